@@ -1,0 +1,243 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X token sampler (one GPU).
+
+Headline: full-vocab nucleus workload, 4096 rows x 3072 fp32 logits, repetition penalty 1.1 over
+512-id histories, temperature 1.0, top-k off, top-p 0.95. A step is one sampler pass over one batch
+with every input already resident in HBM. Inputs rotate over enough distinct copies (> 2x the
+256 MB last-level cache) that each step reads its batch from HBM.
+
+Also reported: single-row talker-step latency host-to-host (p50/p99), the roofline of the sampler
+kernel (algorithmic bytes / HIP-event time on the context stream), HBM traffic from rocprofv3
+counters (committed summary), parity of the timed batch against the CPU oracle, and the CPU oracle's
+throughput on this host as the baseline.
+
+`python bench.py --summarize-trace <kernel_trace.csv>` prints per-(kernel, grid) duration stats of a
+rocprofv3 kernel trace.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import re
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "sampled rows/s + HBM GB/s (% peak) at 4096×3072; p50 µs/step at 1 row"
+LLC_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_full_vocab_nucleus_4096x3072.txt")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def read_traffic():
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, or None."""
+    try:
+        text = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", text)
+    return float(m.group(1)) if m else None
+
+
+def summarize_trace(path: str) -> None:
+    import csv
+    from collections import defaultdict
+
+    groups = defaultdict(list)
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            name = row.get("Kernel_Name") or row.get("KernelName") or row.get("Name")
+            grid = row.get("Grid_Size_X") or row.get("Grid_Size") or "?"
+            wg = row.get("Workgroup_Size_X") or row.get("Workgroup_Size") or "?"
+            dur = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+            groups[(name, grid, wg)].append(dur)
+    print(f"{'calls':>7} {'avg_us':>10} {'median_us':>10} {'min_us':>9} {'max_us':>9}  grid  wg  kernel")
+    for (name, grid, wg), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        d.sort()
+        print(f"{len(d):7d} {sum(d) / len(d) / 1e3:10.3f} {d[len(d) // 2] / 1e3:10.3f} {d[0] / 1e3:9.3f} "
+              f"{d[-1] / 1e3:9.3f}  {grid}  {wg}  {name[:110]}")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5000)
+    ap.add_argument("--warmup", type=int, default=500)
+    ap.add_argument("--latency-steps", type=int, default=10000)
+    ap.add_argument("--cpu-reps", type=int, default=5, help="passes of the CPU oracle over the batch")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
+    ap.add_argument("--summarize-trace", metavar="CSV")
+    args = ap.parse_args()
+
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace)
+        return 0
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (the sampler's rows are "
+              f"independent; sharding is plain row splitting with no communication).", file=sys.stderr)
+        return 2
+
+    import numpy as np
+
+    from voxwerk_amd import hip, workloads
+    from voxwerk_amd.sampler import Context
+
+    w = workloads.workload(4)
+    rows, vocab = w.rows, w.vocab
+    t0 = time.time()
+    batch = w.generate()
+    log(f"[bench] generated {w.name} {rows}x{vocab} in {time.time() - t0:.2f}s digest={batch.digest()[:16]}")
+    bytes_per_step = rows * w.bytes_per_row()
+    in_bytes = batch.logits.nbytes + batch.hist_ids.nbytes
+    nbuf = max(2, math.ceil(2 * LLC_BYTES / in_bytes) + 1)
+
+    ctx = Context(0)
+    stream = ctx.stream()
+    d_logits = [hip.DeviceArray.from_numpy(batch.logits)]
+    d_hist = [hip.DeviceArray.from_numpy(batch.hist_ids)]
+    for _ in range(nbuf - 1):
+        a = hip.DeviceArray(batch.logits.shape, np.float32)
+        a.copy_from(d_logits[0])
+        d_logits.append(a)
+        h = hip.DeviceArray(batch.hist_ids.shape, np.int32)
+        h.copy_from(d_hist[0])
+        d_hist.append(h)
+    d_off = hip.DeviceArray.from_numpy(batch.hist_off)
+    d_params = hip.DeviceArray.from_numpy(batch.params[:1])
+    d_u = hip.DeviceArray.from_numpy(batch.u)
+    d_ids = hip.DeviceArray((rows,), np.int32)
+    log(f"[bench] {nbuf} rotating input copies ({nbuf * in_bytes / 2**20:.0f} MiB)")
+
+    def step(i: int) -> None:
+        k = i % nbuf
+        ctx.sample_device(rows, vocab, d_logits[k], vocab, d_params, 0, d_u, d_ids, d_off, d_hist[k])
+
+    for i in range(args.warmup):
+        step(i)
+    hip.synchronize()
+    ev0, ev1 = hip.Event(), hip.Event()
+    t_wall = time.perf_counter()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    ev1.record(stream)
+    ev1.synchronize()
+    wall = time.perf_counter() - t_wall
+    hip.synchronize()
+    ms = ev0.elapsed_ms(ev1) / args.steps
+    value = rows / (ms / 1e3)
+    gbps = bytes_per_step / (ms / 1e3) / 1e9
+    log(f"[bench] {args.steps} steps: {ms * 1e3:.2f} us/step (events), wall {wall / args.steps * 1e6:.2f} us/step, "
+        f"{value:.4g} rows/s, {gbps:.0f} GB/s")
+
+    # parity of the timed batch (copy 0) against the CPU oracle
+    step(0)
+    hip.synchronize()
+    gpu_ids = d_ids.numpy()
+
+    # single-row talker step, host to host (logits in pageable host memory, id back on the host)
+    w1 = workloads.workload(1)
+    b1 = w1.generate()
+    lat = []
+    for i in range(200 + args.latency_steps):
+        t = time.perf_counter_ns()
+        ctx.sample(b1.logits, b1.params, b1.u, b1.hist_off, b1.hist_ids)
+        if i >= 200:
+            lat.append(time.perf_counter_ns() - t)
+    lat = np.sort(np.array(lat)) / 1e3
+    p50, p99 = float(lat[len(lat) // 2]), float(lat[int(len(lat) * 0.99)])
+    log(f"[bench] talker step 1x3072 host-to-host: p50 {p50:.1f} us, p99 {p99:.1f} us")
+
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        from oracle import ref
+
+        reps = []
+        ora = None
+        for _ in range(max(1, args.cpu_reps)):
+            t = time.perf_counter()
+            ora = ref.sample(batch.logits, batch.params, batch.u, batch.hist_off, batch.hist_ids, threads=1)
+            reps.append(time.perf_counter() - t)
+        cpu_s = sorted(reps)[len(reps) // 2]
+        ncores = os.cpu_count() or 1
+        t = time.perf_counter()
+        ref.sample(batch.logits, batch.params, batch.u, batch.hist_off, batch.hist_ids, threads=ncores, want_info=False)
+        cpu_all_s = time.perf_counter() - t
+        cpu = {
+            "value": rows / cpu_s,
+            "unit": "rows/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"{w.name} {rows}x{vocab}, the whole batch, median of {len(reps)} passes, 1 thread; "
+                      f"C restatement of Sampler.cs semantics (gcc -O2), {cpu_model()}",
+            "all_cores": {"value": rows / cpu_all_s, "unit": "rows/s", "cores": ncores},
+        }
+        parity = ref.classify(gpu_ids, ora)
+        log(f"[bench] cpu oracle {cpu['value']:.0f} rows/s (1 thread), {cpu['all_cores']['value']:.0f} rows/s "
+            f"({ncores} threads); parity {parity}")
+
+    traffic = read_traffic()
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 logits, f64 probabilities",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{w.name}: {rows} rows x {vocab} fp32 logits, repetition penalty 1.1 over 512-id histories, "
+                        f"temperature 1.0, top-k off, top-p 0.95, device-resident inputs",
+            "rows": rows,
+            "vocab": vocab,
+            "hist_len": w.hist_len,
+            "rotating_input_copies": nbuf,
+        },
+        "hbm_gbps": round(gbps, 1),
+        "hbm_pct_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+        "latency_1row_us": {"p50": round(p50, 2), "p99": round(p99, 2), "workload": "talker_step 1x3072 host-to-host"},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": bytes_per_step,
+            "kernel_us": round(ms * 1e3, 3),
+        },
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    print(json.dumps(out), flush=True)
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

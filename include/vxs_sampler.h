@@ -1,0 +1,142 @@
+/*
+ * vxs_sampler.h — C ABI of the MI355X (gfx950) token sampler.
+ *
+ * One call turns each row of fp32 logits into a token id with the semantics of voxwerk's
+ * Sampler (src/Voxwerk/Talker/Sampler.cs:1-96) plus the talker's suppression glue
+ * (src/Voxwerk/Talker/TalkerGenerator.cs:246-249, :370-373):
+ *   repetition penalty -> suppression -> (greedy argmax | temperature -> top-k -> softmax
+ *   -> top-p -> inverse-CDF draw from a caller-supplied uniform).
+ *
+ * The reference is managed C# with no native boundary; these entry points are what its
+ * P/Invoke layer binds (DllImport style of src/Voxwerk/Numerics/NativeBuffer.cs:78-92).
+ * Plain pointers and sizes only. No C++ exceptions cross this boundary.
+ *
+ * Threading: one context owns one HIP stream and may be used by one thread at a time.
+ * Separate contexts may run concurrently.
+ */
+#ifndef VXS_SAMPLER_H
+#define VXS_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define VXS_API __attribute__((visibility("default")))
+#else
+#define VXS_API
+#endif
+
+/* Return codes. A row that fails gets the code in its out_ids slot (all codes are < 0). */
+#define VXS_OK 0
+#define VXS_ERR_INVALID_ARG (-1)     /* bad pointer/shape/option (C#: ArgumentException family)          */
+#define VXS_ERR_ID_OUT_OF_RANGE (-2) /* history id < 0 or >= vocab (C#: Span indexer at Sampler.cs:30)   */
+#define VXS_ERR_NONFINITE (-3)       /* NaN or +inf logit after temperature: outside the contract        */
+#define VXS_ERR_HIP (-4)             /* HIP runtime failure; text in vxs_last_error                      */
+#define VXS_ERR_UNSUPPORTED (-5)     /* shape outside what this build implements; text in vxs_last_error */
+#define VXS_ERR_NO_DEVICE (-6)       /* no usable gfx950 device                                          */
+
+/* flags for vxs_sample / vxs_sample_device */
+#define VXS_FLAG_NONE 0u
+
+/*
+ * Per-row sampling parameters (blittable; 36 bytes, 4-byte aligned).
+ * Mirrors SamplingOptions (Sampler.cs:4-13), GenerationOptions.RepetitionPenalty
+ * (TalkerGenerator.cs:11) and the talker's suppression rule (TalkerGenerator.cs:247-248).
+ */
+typedef struct vxs_params {
+    int32_t do_sample;   /* SamplingOptions.DoSample; 0 = first-index argmax, no draw consumed      */
+    int32_t top_k;       /* SamplingOptions.TopK; applied only when 0 < top_k < vocab               */
+    float top_p;         /* SamplingOptions.TopP; applied only when top_p < 1                       */
+    float temperature;   /* SamplingOptions.Temperature; logits are multiplied by fl32(1/T)         */
+    float rep_penalty;   /* repetition penalty over the distinct history ids; 1 = off               */
+    int32_t supp_begin;  /* ids in [supp_begin, supp_end) except keep_id are set to -inf            */
+    int32_t supp_end;    /*   (talker: [vocab-1024, vocab) except EOS); empty range = off           */
+    int32_t keep_id;     /* exempt from suppression (EOS); -1 = none                                */
+    int32_t ban_id;      /* set to -inf after suppression (EOS while step < 2); -1 = none           */
+} vxs_params;
+
+typedef struct vxs_ctx vxs_ctx;
+
+/*
+ * Create a context on HIP device `device` (ordinal among visible devices). Capacities are
+ * hints: buffers grow on demand and are freed by vxs_destroy.
+ * Replaces: construction of Sampler (Sampler.cs:21) — the RNG stays with the caller, which
+ * passes one NextDouble() per sampled row as `u`.
+ */
+VXS_API int vxs_create(vxs_ctx** out, int device, int max_rows, int max_vocab, int64_t max_hist);
+VXS_API void vxs_destroy(vxs_ctx* ctx);
+
+/* Text of the last error on this context ("" if none). Valid until the next call on ctx. */
+VXS_API const char* vxs_last_error(const vxs_ctx* ctx);
+
+/* Library version string, e.g. "vxs 0.1.0 gfx950". */
+VXS_API const char* vxs_version(void);
+
+/*
+ * Use an external HIP stream (hipStream_t passed as void*) for all work of this context.
+ * NULL restores the context's own stream. The caller keeps ownership of the stream.
+ */
+VXS_API int vxs_set_stream(vxs_ctx* ctx, void* hip_stream);
+/* The hipStream_t (as void*) this context currently launches on. */
+VXS_API void* vxs_get_stream(const vxs_ctx* ctx);
+
+/*
+ * Host-pointer sampling call; synchronous.
+ * Replaces, for each row: Sampler.ApplyRepetitionPenalty (Sampler.cs:25-33), the suppression
+ * loops (TalkerGenerator.cs:247-248, :371-372) and Sampler.Select (Sampler.cs:35-88) as
+ * called at TalkerGenerator.cs:246-249, :268, :370-373, :419-420.
+ *
+ *   logits     [rows][ld] fp32, host memory; only the first `vocab` entries of a row are read
+ *   hist_off   [rows+1] CSR offsets into hist_ids (hist_off[0] need not be 0); NULL = no history
+ *   hist_ids   int32 generated-code history; duplicates allowed (applied once per distinct id)
+ *   params     params[r * params_stride]; params_stride 0 broadcasts one struct to all rows
+ *   u          [rows] uniforms in [0,1) (Random.NextDouble() per sampled row); may be NULL
+ *              when no row samples
+ *   out_ids    [rows] sampled ids; a failing row receives its negative error code
+ *   out_logits NULL or [rows][vocab]: the row as Select leaves the caller's span (after
+ *              penalty, suppression, temperature and the top-k -inf mask)
+ *   out_probs  NULL or [rows][vocab] fp64: final probabilities the draw used (parity/debug)
+ * Returns VXS_OK, or the first (lowest row) error code.
+ */
+VXS_API int vxs_sample(vxs_ctx* ctx, int rows, int vocab, const float* logits, int64_t ld,
+                       const int32_t* hist_off, const int32_t* hist_ids,
+                       const vxs_params* params, int params_stride, const double* u,
+                       int32_t* out_ids, float* out_logits, double* out_probs, uint32_t flags);
+
+/*
+ * Device-pointer sampling call; asynchronous on the context stream. Every pointer is device
+ * memory (params included). Per-row errors land in out_ids as negative codes; call
+ * vxs_synchronize to wait. For callers whose logits are already resident on the GPU (logit
+ * heads on device) and for kernel-only timing.
+ */
+VXS_API int vxs_sample_device(vxs_ctx* ctx, int rows, int vocab, const float* d_logits, int64_t ld,
+                              const int32_t* d_hist_off, const int32_t* d_hist_ids,
+                              const vxs_params* d_params, int params_stride, const double* d_u,
+                              int32_t* d_out_ids, float* d_out_logits, double* d_out_probs,
+                              uint32_t flags);
+
+/* Wait for all work queued on the context stream. */
+VXS_API int vxs_synchronize(vxs_ctx* ctx);
+
+/*
+ * In-place repetition penalty on host rows (Sampler.ApplyRepetitionPenalty, Sampler.cs:25-33):
+ * each distinct history id's logit s becomes s*penalty if s < 0, else s/penalty.
+ * penalty == 1 is a no-op. Synchronous.
+ */
+VXS_API int vxs_apply_repetition_penalty(vxs_ctx* ctx, int rows, int vocab, float* logits, int64_t ld,
+                                         const int32_t* hist_off, const int32_t* hist_ids,
+                                         float penalty);
+
+/* First index of the maximum of each host row (Sampler.ArgMax, Sampler.cs:90-95). Synchronous. */
+VXS_API int vxs_argmax(vxs_ctx* ctx, int rows, int vocab, const float* logits, int64_t ld,
+                       int32_t* out_ids);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VXS_SAMPLER_H */

@@ -1,0 +1,83 @@
+"""Build recipe: the gfx950 HIP library, the CPU workload generator, and (for tests) the C++ facade
+test program. ``python -m voxwerk_amd.build`` or ``__graft_entry__.build()``.
+
+HIP code is compiled with -ffp-contract=off (every fp32/fp64 op of the sampler is a single IEEE
+operation, as in the reference's managed code) and with packed-FP32 instructions disabled.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+LIB = os.path.join(PKG, "lib")
+INCLUDE = os.path.join(REPO, "include")
+
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+ARCH = "gfx950"
+
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    f"-I{INCLUDE}",
+]
+HIP_SOURCES = ["vxs_kernels.hip", "vxs_api.cpp"]
+
+
+def _run(cmd: list[str], cwd: str = REPO) -> None:
+    print("+ " + " ".join(cmd), flush=True)
+    p = subprocess.run(cmd, cwd=cwd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in p.stdout.splitlines() if "packed-fp32-ops" not in l and l.strip())
+    if out:
+        print(out, flush=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"build step failed ({p.returncode}): {' '.join(cmd)}")
+
+
+def build_hip() -> str:
+    os.makedirs(LIB, exist_ok=True)
+    out = os.path.join(LIB, "libvxs.so")
+    tmp = out + ".tmp"
+    _run([HIPCC, *HIP_FLAGS, "-shared", "-o", tmp, *[os.path.join(CSRC, s) for s in HIP_SOURCES]])
+    os.replace(tmp, out)
+    return out
+
+
+def build_synth() -> str:
+    os.makedirs(LIB, exist_ok=True)
+    out = os.path.join(LIB, "libvxs_synth.so")
+    _run(["gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-Wall", "-Wextra", "-ffp-contract=off",
+          "-fno-fast-math", "-pthread", "-o", out, os.path.join(CSRC, "vxs_synth.c"), "-lm"])
+    return out
+
+
+def build_facade_test() -> str:
+    """C++ program exercising include/voxwerk/Sampler.hpp against libvxs.so (run by a GPU test)."""
+    src = os.path.join(REPO, "tests", "cpp", "test_facade.cpp")
+    out = os.path.join(REPO, "tests", "cpp", "test_facade")
+    _run(["g++", "-O2", "-std=c++17", "-Wall", f"-I{INCLUDE}", "-o", out, src, f"-L{LIB}", "-lvxs",
+          f"-Wl,-rpath,{LIB}", "-Wl,-rpath,$ORIGIN/../../voxwerk_amd/lib"])
+    return out
+
+
+def build_all(with_tests: bool = True) -> None:
+    if not os.path.exists(HIPCC) and not shutil.which("hipcc"):
+        raise RuntimeError("hipcc not found: a ROCm toolchain is required")
+    build_synth()
+    build_hip()
+    if with_tests and os.path.exists(os.path.join(REPO, "tests", "cpp", "test_facade.cpp")):
+        build_facade_test()
+
+
+if __name__ == "__main__":
+    build_all(with_tests="--no-tests" not in sys.argv)

@@ -1,0 +1,426 @@
+// vxs_api.cpp — the C ABI of include/vxs_sampler.h: contexts, device buffers, pinned staging,
+// argument validation and error mapping. No C++ exception crosses the boundary.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "vxs_internal.h"
+
+namespace {
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
+
+// Device buffer that only grows.
+struct DevBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    hipError_t reserve(size_t n) {
+        if (n <= cap) return hipSuccess;
+        if (p) {
+            hipError_t e = hipFree(p);
+            p = nullptr;
+            cap = 0;
+            if (e != hipSuccess) return e;
+        }
+        size_t want = std::max(n, cap + cap / 2);
+        hipError_t e = hipMalloc(&p, want);
+        if (e != hipSuccess) return e;
+        cap = want;
+        return hipSuccess;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
+// Pinned host buffer that only grows.
+struct HostBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    hipError_t reserve(size_t n) {
+        if (n <= cap) return hipSuccess;
+        if (p) {
+            hipError_t e = hipHostFree(p);
+            p = nullptr;
+            cap = 0;
+            if (e != hipSuccess) return e;
+        }
+        size_t want = std::max(n, cap + cap / 2);
+        hipError_t e = hipHostMalloc(&p, want, hipHostMallocDefault);
+        if (e != hipSuccess) return e;
+        cap = want;
+        return hipSuccess;
+    }
+    void release() {
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
+}  // namespace
+
+struct vxs_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    std::string err;
+    DevBuf d_in, d_ids, d_logits_out, d_probs_out;
+    HostBuf h_in, h_ids, h_out;
+};
+
+namespace {
+
+int fail(vxs_ctx* ctx, int code, const std::string& msg) {
+    if (ctx) ctx->err = msg;
+    return code;
+}
+
+int hip_fail(vxs_ctx* ctx, hipError_t e, const char* what) {
+    std::string m = std::string(what) + ": " + hipGetErrorString(e);
+    return fail(ctx, VXS_ERR_HIP, m);
+}
+
+#define VXS_HIP(ctx, call)                                         \
+    do {                                                           \
+        hipError_t e_ = (call);                                    \
+        if (e_ != hipSuccess) return hip_fail((ctx), e_, #call);   \
+    } while (0)
+
+const char* code_text(int code) {
+    switch (code) {
+        case VXS_ERR_INVALID_ARG: return "invalid argument";
+        case VXS_ERR_ID_OUT_OF_RANGE: return "history id out of range [0, vocab)";
+        case VXS_ERR_NONFINITE: return "NaN or +inf logit after temperature";
+        case VXS_ERR_HIP: return "HIP error";
+        case VXS_ERR_UNSUPPORTED: return "unsupported shape";
+        case VXS_ERR_NO_DEVICE: return "no gfx950 device";
+        default: return "error";
+    }
+}
+
+// Validation shared by the host and device entry points (host-side facts only).
+int check_shape(vxs_ctx* ctx, int rows, int vocab, const void* logits, int64_t ld, const void* params,
+                int params_stride, const void* out_ids) {
+    if (!ctx) return VXS_ERR_INVALID_ARG;
+    if (rows < 0) return fail(ctx, VXS_ERR_INVALID_ARG, "rows < 0");
+    if (vocab <= 0) return fail(ctx, VXS_ERR_INVALID_ARG, "vocab <= 0");
+    if (ld < vocab) return fail(ctx, VXS_ERR_INVALID_ARG, "ld < vocab");
+    if (params_stride < 0) return fail(ctx, VXS_ERR_INVALID_ARG, "params_stride < 0");
+    if (rows > 0 && (!logits || !params || !out_ids))
+        return fail(ctx, VXS_ERR_INVALID_ARG, "null logits, params or out_ids");
+    if (vocab > vxs::kRowResidentMaxVocab)
+        return fail(ctx, VXS_ERR_UNSUPPORTED,
+                    "vocab " + std::to_string(vocab) + " exceeds the row-resident limit " +
+                        std::to_string(vxs::kRowResidentMaxVocab));
+    return VXS_OK;
+}
+
+int check_params_host(vxs_ctx* ctx, int rows, const vxs_params* params, int stride, const double* u) {
+    const int np = stride == 0 ? 1 : rows;
+    for (int i = 0; i < np; i++) {
+        const vxs_params& p = params[(int64_t)i * stride];
+        if (p.do_sample && !u) return fail(ctx, VXS_ERR_INVALID_ARG, "u is NULL but a row samples");
+    }
+    return VXS_OK;
+}
+
+int first_row_error(vxs_ctx* ctx, const int32_t* ids, int rows) {
+    for (int r = 0; r < rows; r++)
+        if (ids[r] < 0) {
+            char buf[96];
+            std::snprintf(buf, sizeof buf, "row %d: %s", r, code_text(ids[r]));
+            return fail(ctx, ids[r], buf);
+        }
+    return VXS_OK;
+}
+
+// Pack host inputs into the pinned staging block; returns byte offsets of each section.
+struct Layout {
+    size_t params, u, hoff, hids, logits, total;
+    int64_t ld_dev;
+    int np;
+    int64_t nh;
+};
+
+Layout plan(int rows, int vocab, int params_stride, const int32_t* hist_off) {
+    Layout L{};
+    L.np = params_stride == 0 ? 1 : rows;
+    L.nh = hist_off ? (int64_t)hist_off[rows] - hist_off[0] : 0;
+    L.ld_dev = ((int64_t)vocab + 3) & ~(int64_t)3;
+    size_t off = 0;
+    L.params = off;
+    off = align_up(off + sizeof(vxs_params) * (size_t)std::max(L.np, 1));
+    L.u = off;
+    off = align_up(off + sizeof(double) * (size_t)rows);
+    L.hoff = off;
+    off = align_up(off + sizeof(int32_t) * (size_t)(rows + 1));
+    L.hids = off;
+    off = align_up(off + sizeof(int32_t) * (size_t)L.nh);
+    L.logits = off;
+    off = align_up(off + sizeof(float) * (size_t)rows * (size_t)L.ld_dev);
+    L.total = off;
+    return L;
+}
+
+int check_hist_host(vxs_ctx* ctx, int rows, const int32_t* hist_off, const int32_t* hist_ids) {
+    if (!hist_off) return VXS_OK;
+    for (int r = 0; r < rows; r++)
+        if (hist_off[r + 1] < hist_off[r]) return fail(ctx, VXS_ERR_INVALID_ARG, "hist_off not monotone");
+    if (hist_off[rows] > hist_off[0] && !hist_ids) return fail(ctx, VXS_ERR_INVALID_ARG, "hist_ids is NULL");
+    return VXS_OK;
+}
+
+// Stage inputs and launch. On success the kernel is queued on ctx->stream.
+int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int64_t ld, const int32_t* hist_off,
+                     const int32_t* hist_ids, const vxs_params* params, int params_stride, const double* u,
+                     bool want_logits, bool want_probs, uint32_t kflags) {
+    const Layout L = plan(rows, vocab, params_stride, hist_off);
+    VXS_HIP(ctx, ctx->h_in.reserve(L.total));
+    VXS_HIP(ctx, ctx->d_in.reserve(L.total));
+    char* h = static_cast<char*>(ctx->h_in.p);
+    for (int i = 0; i < L.np; i++)
+        std::memcpy(h + L.params + sizeof(vxs_params) * i, params + (int64_t)i * params_stride, sizeof(vxs_params));
+    if (u) std::memcpy(h + L.u, u, sizeof(double) * rows);
+    else std::memset(h + L.u, 0, sizeof(double) * rows);
+    int32_t* hoff = reinterpret_cast<int32_t*>(h + L.hoff);
+    if (hist_off) {
+        for (int r = 0; r <= rows; r++) hoff[r] = hist_off[r] - hist_off[0];
+        if (L.nh) std::memcpy(h + L.hids, hist_ids + hist_off[0], sizeof(int32_t) * L.nh);
+    }
+    float* lg = reinterpret_cast<float*>(h + L.logits);
+    if (ld == L.ld_dev) {
+        std::memcpy(lg, logits, sizeof(float) * (size_t)rows * (size_t)ld);
+    } else {
+        for (int r = 0; r < rows; r++) std::memcpy(lg + (int64_t)r * L.ld_dev, logits + (int64_t)r * ld, sizeof(float) * vocab);
+    }
+    VXS_HIP(ctx, ctx->d_ids.reserve(sizeof(int32_t) * (size_t)rows));
+    if (want_logits) VXS_HIP(ctx, ctx->d_logits_out.reserve(sizeof(float) * (size_t)rows * vocab));
+    if (want_probs) VXS_HIP(ctx, ctx->d_probs_out.reserve(sizeof(double) * (size_t)rows * vocab));
+    VXS_HIP(ctx, hipMemcpyAsync(ctx->d_in.p, ctx->h_in.p, L.total, hipMemcpyHostToDevice, ctx->stream));
+
+    char* d = static_cast<char*>(ctx->d_in.p);
+    vxs::SampleArgs a{};
+    a.rows = rows;
+    a.vocab = vocab;
+    a.ld = L.ld_dev;
+    a.logits = reinterpret_cast<const float*>(d + L.logits);
+    a.hist_off = hist_off ? reinterpret_cast<const int32_t*>(d + L.hoff) : nullptr;
+    a.hist_ids = reinterpret_cast<const int32_t*>(d + L.hids);
+    a.params = reinterpret_cast<const vxs_params*>(d + L.params);
+    a.params_stride = params_stride == 0 ? 0 : 1;
+    a.u = reinterpret_cast<const double*>(d + L.u);
+    a.out_ids = static_cast<int32_t*>(ctx->d_ids.p);
+    a.out_logits = want_logits ? static_cast<float*>(ctx->d_logits_out.p) : nullptr;
+    a.out_probs = want_probs ? static_cast<double*>(ctx->d_probs_out.p) : nullptr;
+    a.kflags = kflags;
+    VXS_HIP(ctx, vxs::launch_sample(a, ctx->stream));
+    return VXS_OK;
+}
+
+// Copy `bytes` of device results into host memory through pinned staging.
+int fetch(vxs_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (!bytes) return VXS_OK;
+    VXS_HIP(ctx, ctx->h_out.reserve(bytes));
+    VXS_HIP(ctx, hipMemcpyAsync(ctx->h_out.p, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    VXS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    std::memcpy(dst, ctx->h_out.p, bytes);
+    return VXS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+VXS_API const char* vxs_version(void) { return "vxs 0.1.0 gfx950"; }
+
+VXS_API int vxs_create(vxs_ctx** out, int device, int max_rows, int max_vocab, int64_t max_hist) {
+    if (!out) return VXS_ERR_INVALID_ARG;
+    *out = nullptr;
+    if (max_rows < 0 || max_vocab < 0 || max_hist < 0) return VXS_ERR_INVALID_ARG;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return VXS_ERR_NO_DEVICE;
+    if (device < 0 || device >= n) return VXS_ERR_NO_DEVICE;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return VXS_ERR_NO_DEVICE;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return VXS_ERR_NO_DEVICE;
+    vxs_ctx* ctx = new (std::nothrow) vxs_ctx();
+    if (!ctx) return VXS_ERR_INVALID_ARG;
+    ctx->device = device;
+    if (hipSetDevice(device) != hipSuccess ||
+        hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess) {
+        delete ctx;
+        return VXS_ERR_HIP;
+    }
+    ctx->stream = ctx->own_stream;
+    if (max_rows > 0 && max_vocab > 0) {
+        const int32_t* no_hist = nullptr;
+        Layout L = plan(max_rows, max_vocab, 1, no_hist);
+        size_t hist_bytes = align_up(sizeof(int32_t) * (size_t)max_hist);
+        if (ctx->d_in.reserve(L.total + hist_bytes) != hipSuccess || ctx->h_in.reserve(L.total + hist_bytes) != hipSuccess ||
+            ctx->d_ids.reserve(sizeof(int32_t) * (size_t)max_rows) != hipSuccess ||
+            ctx->h_out.reserve(sizeof(int32_t) * (size_t)max_rows) != hipSuccess) {
+            vxs_destroy(ctx);
+            return VXS_ERR_HIP;
+        }
+    }
+    *out = ctx;
+    return VXS_OK;
+}
+
+VXS_API void vxs_destroy(vxs_ctx* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    ctx->d_in.release();
+    ctx->d_ids.release();
+    ctx->d_logits_out.release();
+    ctx->d_probs_out.release();
+    ctx->h_in.release();
+    ctx->h_ids.release();
+    ctx->h_out.release();
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+}
+
+VXS_API const char* vxs_last_error(const vxs_ctx* ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+VXS_API int vxs_set_stream(vxs_ctx* ctx, void* hip_stream) {
+    if (!ctx) return VXS_ERR_INVALID_ARG;
+    ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+    return VXS_OK;
+}
+
+VXS_API void* vxs_get_stream(const vxs_ctx* ctx) { return ctx ? static_cast<void*>(ctx->stream) : nullptr; }
+
+VXS_API int vxs_synchronize(vxs_ctx* ctx) {
+    if (!ctx) return VXS_ERR_INVALID_ARG;
+    VXS_HIP(ctx, hipSetDevice(ctx->device));
+    VXS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return VXS_OK;
+}
+
+VXS_API int vxs_sample(vxs_ctx* ctx, int rows, int vocab, const float* logits, int64_t ld, const int32_t* hist_off,
+                       const int32_t* hist_ids, const vxs_params* params, int params_stride, const double* u,
+                       int32_t* out_ids, float* out_logits, double* out_probs, uint32_t flags) {
+    try {
+        int rc = check_shape(ctx, rows, vocab, logits, ld, params, params_stride, out_ids);
+        if (rc != VXS_OK) return rc;
+        if (flags != VXS_FLAG_NONE) return fail(ctx, VXS_ERR_INVALID_ARG, "unknown flags");
+        if (rows == 0) return VXS_OK;
+        if ((rc = check_params_host(ctx, rows, params, params_stride, u)) != VXS_OK) return rc;
+        if ((rc = check_hist_host(ctx, rows, hist_off, hist_ids)) != VXS_OK) return rc;
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        rc = stage_and_launch(ctx, rows, vocab, logits, ld, hist_off, hist_ids, params, params_stride, u,
+                              out_logits != nullptr, out_probs != nullptr, 0);
+        if (rc != VXS_OK) return rc;
+        if ((rc = fetch(ctx, out_ids, ctx->d_ids.p, sizeof(int32_t) * (size_t)rows)) != VXS_OK) return rc;
+        if (out_logits && (rc = fetch(ctx, out_logits, ctx->d_logits_out.p, sizeof(float) * (size_t)rows * vocab)) != VXS_OK)
+            return rc;
+        if (out_probs && (rc = fetch(ctx, out_probs, ctx->d_probs_out.p, sizeof(double) * (size_t)rows * vocab)) != VXS_OK)
+            return rc;
+        ctx->err.clear();
+        return first_row_error(ctx, out_ids, rows);
+    } catch (const std::exception& e) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, e.what());
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
+VXS_API int vxs_sample_device(vxs_ctx* ctx, int rows, int vocab, const float* d_logits, int64_t ld,
+                              const int32_t* d_hist_off, const int32_t* d_hist_ids, const vxs_params* d_params,
+                              int params_stride, const double* d_u, int32_t* d_out_ids, float* d_out_logits,
+                              double* d_out_probs, uint32_t flags) {
+    try {
+        int rc = check_shape(ctx, rows, vocab, d_logits, ld, d_params, params_stride, d_out_ids);
+        if (rc != VXS_OK) return rc;
+        if (flags != VXS_FLAG_NONE) return fail(ctx, VXS_ERR_INVALID_ARG, "unknown flags");
+        if (rows == 0) return VXS_OK;
+        if (d_hist_off && !d_hist_ids) return fail(ctx, VXS_ERR_INVALID_ARG, "hist_ids is NULL");
+        if (params_stride > 1) return fail(ctx, VXS_ERR_INVALID_ARG, "device params_stride must be 0 or 1");
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        vxs::SampleArgs a{};
+        a.rows = rows;
+        a.vocab = vocab;
+        a.ld = ld;
+        a.logits = d_logits;
+        a.hist_off = d_hist_off;
+        a.hist_ids = d_hist_ids;
+        a.params = d_params;
+        a.params_stride = params_stride;
+        a.u = d_u;
+        a.out_ids = d_out_ids;
+        a.out_logits = d_out_logits;
+        a.out_probs = d_out_probs;
+        a.kflags = 0;
+        VXS_HIP(ctx, vxs::launch_sample(a, ctx->stream));
+        ctx->err.clear();
+        return VXS_OK;
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
+VXS_API int vxs_apply_repetition_penalty(vxs_ctx* ctx, int rows, int vocab, float* logits, int64_t ld,
+                                         const int32_t* hist_off, const int32_t* hist_ids, float penalty) {
+    try {
+        vxs_params p{};
+        p.do_sample = 0;
+        p.rep_penalty = penalty;
+        p.keep_id = -1;
+        p.ban_id = -1;
+        int32_t dummy = 0;
+        int rc = check_shape(ctx, rows, vocab, logits, ld, &p, 0, &dummy);
+        if (rc != VXS_OK) return rc;
+        if (rows == 0 || penalty == 1.0f || !hist_off) return VXS_OK;  // Sampler.cs:27
+        if ((rc = check_hist_host(ctx, rows, hist_off, hist_ids)) != VXS_OK) return rc;
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        rc = stage_and_launch(ctx, rows, vocab, logits, ld, hist_off, hist_ids, &p, 0, nullptr, true, false,
+                              vxs::KF_STOP_AFTER_PENALTY);
+        if (rc != VXS_OK) return rc;
+        VXS_HIP(ctx, ctx->h_ids.reserve(sizeof(int32_t) * (size_t)rows));
+        if ((rc = fetch(ctx, ctx->h_ids.p, ctx->d_ids.p, sizeof(int32_t) * (size_t)rows)) != VXS_OK) return rc;
+        ctx->err.clear();
+        if ((rc = first_row_error(ctx, static_cast<int32_t*>(ctx->h_ids.p), rows)) != VXS_OK) return rc;
+        const size_t row_bytes = sizeof(float) * (size_t)vocab;
+        VXS_HIP(ctx, ctx->h_out.reserve(row_bytes * rows));
+        VXS_HIP(ctx, hipMemcpyAsync(ctx->h_out.p, ctx->d_logits_out.p, row_bytes * rows, hipMemcpyDeviceToHost, ctx->stream));
+        VXS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        for (int r = 0; r < rows; r++)
+            std::memcpy(logits + (int64_t)r * ld, static_cast<char*>(ctx->h_out.p) + row_bytes * r, row_bytes);
+        return VXS_OK;
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
+VXS_API int vxs_argmax(vxs_ctx* ctx, int rows, int vocab, const float* logits, int64_t ld, int32_t* out_ids) {
+    try {
+        vxs_params p{};
+        p.do_sample = 0;
+        p.rep_penalty = 1.0f;
+        p.keep_id = -1;
+        p.ban_id = -1;
+        int rc = check_shape(ctx, rows, vocab, logits, ld, &p, 0, out_ids);
+        if (rc != VXS_OK) return rc;
+        if (rows == 0) return VXS_OK;
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        rc = stage_and_launch(ctx, rows, vocab, logits, ld, nullptr, nullptr, &p, 0, nullptr, false, false, 0);
+        if (rc != VXS_OK) return rc;
+        if ((rc = fetch(ctx, out_ids, ctx->d_ids.p, sizeof(int32_t) * (size_t)rows)) != VXS_OK) return rc;
+        ctx->err.clear();
+        return first_row_error(ctx, out_ids, rows);
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
+}  // extern "C"
