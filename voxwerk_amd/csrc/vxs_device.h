@@ -1,0 +1,228 @@
+// vxs_device.h — gfx950 device primitives of the sampler: DPP wave scans/reductions, group
+// (W-wave) combines, order-preserving keys, exact 2^-F fixed-point masses, the correctly rounded
+// penalty division and the fp32 exponential used for full-vocabulary masses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vxs {
+namespace dev {
+
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kPosInf = __builtin_huge_valf();
+
+// ---- DPP (gfx9 encodings) ------------------------------------------------------------------
+enum : int {
+    kRowShr1 = 0x111,
+    kRowShr2 = 0x112,
+    kRowShr4 = 0x114,
+    kRowShr8 = 0x118,
+    kRowBcast15 = 0x142,
+    kRowBcast31 = 0x143,
+};
+
+// Lane value moved by DPP; lanes whose source is outside the row/mask keep `old`.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp(uint32_t old, uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)x, CTRL, ROW_MASK, 0xf, false);
+}
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint64_t dpp64(uint64_t old, uint64_t x) {
+    const uint32_t lo = dpp<CTRL, ROW_MASK>((uint32_t)old, (uint32_t)x);
+    const uint32_t hi = dpp<CTRL, ROW_MASK>((uint32_t)(old >> 32), (uint32_t)(x >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint32_t readlane(uint32_t x, int lane) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)x, lane);
+}
+__device__ __forceinline__ uint64_t readlane64(uint64_t x, int lane) {
+    return ((uint64_t)readlane((uint32_t)(x >> 32), lane) << 32) | readlane((uint32_t)x, lane);
+}
+
+// Inclusive prefix sum over the 64 lanes (Hillis-Steele inside rows of 16, then row broadcasts).
+__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t x) {
+    x += dpp<kRowShr1>(0, x);
+    x += dpp<kRowShr2>(0, x);
+    x += dpp<kRowShr4>(0, x);
+    x += dpp<kRowShr8>(0, x);
+    x += dpp<kRowBcast15, 0xa>(0, x);
+    x += dpp<kRowBcast31, 0xc>(0, x);
+    return x;
+}
+__device__ __forceinline__ uint64_t wave_incl_sum(uint64_t x) {
+    x += dpp64<kRowShr1>(0, x);
+    x += dpp64<kRowShr2>(0, x);
+    x += dpp64<kRowShr4>(0, x);
+    x += dpp64<kRowShr8>(0, x);
+    x += dpp64<kRowBcast15, 0xa>(0, x);
+    x += dpp64<kRowBcast31, 0xc>(0, x);
+    return x;
+}
+__device__ __forceinline__ uint32_t wave_sum(uint32_t x) { return readlane(wave_incl_sum(x), 63); }
+__device__ __forceinline__ uint64_t wave_sum(uint64_t x) { return readlane64(wave_incl_sum(x), 63); }
+
+__device__ __forceinline__ double wave_incl_sum(double x) {
+#define VXS_FSTEP(C, M) \
+    x += __longlong_as_double((long long)dpp64<C, M>(0, (uint64_t)__double_as_longlong(x)));
+    VXS_FSTEP(kRowShr1, 0xf)
+    VXS_FSTEP(kRowShr2, 0xf)
+    VXS_FSTEP(kRowShr4, 0xf)
+    VXS_FSTEP(kRowShr8, 0xf)
+    VXS_FSTEP(kRowBcast15, 0xa)
+    VXS_FSTEP(kRowBcast31, 0xc)
+#undef VXS_FSTEP
+    return x;
+}
+__device__ __forceinline__ double readlane_d(double x, int lane) {
+    return __longlong_as_double((long long)readlane64((uint64_t)__double_as_longlong(x), lane));
+}
+__device__ __forceinline__ double wave_sum(double x) { return readlane_d(wave_incl_sum(x), 63); }
+
+#define VXS_MSTEP(OP, IDENT, C, M) x = OP(x, __uint_as_float(dpp<C, M>(__float_as_uint(IDENT), __float_as_uint(x))));
+__device__ __forceinline__ float wave_max(float x) {
+    VXS_MSTEP(fmaxf, kNegInf, kRowShr1, 0xf)
+    VXS_MSTEP(fmaxf, kNegInf, kRowShr2, 0xf)
+    VXS_MSTEP(fmaxf, kNegInf, kRowShr4, 0xf)
+    VXS_MSTEP(fmaxf, kNegInf, kRowShr8, 0xf)
+    VXS_MSTEP(fmaxf, kNegInf, kRowBcast15, 0xa)
+    VXS_MSTEP(fmaxf, kNegInf, kRowBcast31, 0xc)
+    return __uint_as_float(readlane(__float_as_uint(x), 63));
+}
+__device__ __forceinline__ float wave_min(float x) {
+    VXS_MSTEP(fminf, kPosInf, kRowShr1, 0xf)
+    VXS_MSTEP(fminf, kPosInf, kRowShr2, 0xf)
+    VXS_MSTEP(fminf, kPosInf, kRowShr4, 0xf)
+    VXS_MSTEP(fminf, kPosInf, kRowShr8, 0xf)
+    VXS_MSTEP(fminf, kPosInf, kRowBcast15, 0xa)
+    VXS_MSTEP(fminf, kPosInf, kRowBcast31, 0xc)
+    return __uint_as_float(readlane(__float_as_uint(x), 63));
+}
+#undef VXS_MSTEP
+
+#define VXS_USTEP(OP, IDENT, C, M) x = OP(x, dpp<C, M>(IDENT, x));
+__device__ __forceinline__ uint32_t wave_umax(uint32_t x) {
+    VXS_USTEP(max, 0u, kRowShr1, 0xf)
+    VXS_USTEP(max, 0u, kRowShr2, 0xf)
+    VXS_USTEP(max, 0u, kRowShr4, 0xf)
+    VXS_USTEP(max, 0u, kRowShr8, 0xf)
+    VXS_USTEP(max, 0u, kRowBcast15, 0xa)
+    VXS_USTEP(max, 0u, kRowBcast31, 0xc)
+    return readlane(x, 63);
+}
+__device__ __forceinline__ uint32_t wave_umin(uint32_t x) {
+    VXS_USTEP(min, 0xffffffffu, kRowShr1, 0xf)
+    VXS_USTEP(min, 0xffffffffu, kRowShr2, 0xf)
+    VXS_USTEP(min, 0xffffffffu, kRowShr4, 0xf)
+    VXS_USTEP(min, 0xffffffffu, kRowShr8, 0xf)
+    VXS_USTEP(min, 0xffffffffu, kRowBcast15, 0xa)
+    VXS_USTEP(min, 0xffffffffu, kRowBcast31, 0xc)
+    return readlane(x, 63);
+}
+#undef VXS_USTEP
+
+// Max value with the lowest index among equal values (Sampler.ArgMax tie rule).
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#define VXS_ASTEP(C, M)                                                                \
+    {                                                                                  \
+        const float ov = __uint_as_float(dpp<C, M>(__float_as_uint(kNegInf), __float_as_uint(v))); \
+        const int oi = (int)dpp<C, M>(0x7fffffffu, (uint32_t)i);                       \
+        if (ov > v || (ov == v && oi < i)) {                                           \
+            v = ov;                                                                    \
+            i = oi;                                                                    \
+        }                                                                              \
+    }
+    VXS_ASTEP(kRowShr1, 0xf)
+    VXS_ASTEP(kRowShr2, 0xf)
+    VXS_ASTEP(kRowShr4, 0xf)
+    VXS_ASTEP(kRowShr8, 0xf)
+    VXS_ASTEP(kRowBcast15, 0xa)
+    VXS_ASTEP(kRowBcast31, 0xc)
+#undef VXS_ASTEP
+    v = __uint_as_float(readlane(__float_as_uint(v), 63));
+    i = (int)readlane((uint32_t)i, 63);
+}
+
+__device__ __forceinline__ bool wave_any(bool p) { return __ballot(p) != 0; }
+
+// Order-preserving int image of a non-NaN float (for signed-int max/min): negative values get
+// their magnitude bits flipped. The DPP max/min on this image fuses into one instruction per step.
+__device__ __forceinline__ int f2ord(float x) {
+    const int k = __float_as_int(x);
+    return k ^ ((k >> 31) & 0x7fffffff);
+}
+__device__ __forceinline__ float ord2f(int k) { return __int_as_float(k ^ ((k >> 31) & 0x7fffffff)); }
+
+#define VXS_ISTEP(OP, IDENT, C, M) x = OP(x, (int)dpp<C, M>((uint32_t)(IDENT), (uint32_t)x));
+__device__ __forceinline__ int wave_imax_ord(int x) {
+    VXS_ISTEP(max, 0x80000000, kRowShr1, 0xf)
+    VXS_ISTEP(max, 0x80000000, kRowShr2, 0xf)
+    VXS_ISTEP(max, 0x80000000, kRowShr4, 0xf)
+    VXS_ISTEP(max, 0x80000000, kRowShr8, 0xf)
+    VXS_ISTEP(max, 0x80000000, kRowBcast15, 0xa)
+    VXS_ISTEP(max, 0x80000000, kRowBcast31, 0xc)
+    return (int)readlane((uint32_t)x, 63);
+}
+__device__ __forceinline__ int wave_imin_ord(int x) {
+    VXS_ISTEP(min, 0x7fffffff, kRowShr1, 0xf)
+    VXS_ISTEP(min, 0x7fffffff, kRowShr2, 0xf)
+    VXS_ISTEP(min, 0x7fffffff, kRowShr4, 0xf)
+    VXS_ISTEP(min, 0x7fffffff, kRowShr8, 0xf)
+    VXS_ISTEP(min, 0x7fffffff, kRowBcast15, 0xa)
+    VXS_ISTEP(min, 0x7fffffff, kRowBcast31, 0xc)
+    return (int)readlane((uint32_t)x, 63);
+}
+#undef VXS_ISTEP
+// max / min of non-NaN floats over the wave
+__device__ __forceinline__ float wave_fmax(float x) { return ord2f(wave_imax_ord(f2ord(x))); }
+__device__ __forceinline__ float wave_fmin(float x) { return ord2f(wave_imin_ord(f2ord(x))); }
+
+// ---- keys, fixed point, arithmetic ----------------------------------------------------------
+// Order-preserving u32 image of a float; -0 maps to +0 (C# compares them equal).
+__device__ __forceinline__ uint32_t f2key(float f) {
+    if (f == 0.0f) f = 0.0f;
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key2f(uint32_t k) {
+    const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+    return __uint_as_float(u);
+}
+
+// round(e * 2^F) as an integer-valued double, for 0 <= e * 2^F < 2^52. Masses in this form add
+// exactly (every partial sum stays an integer below 2^53), so sums and LDS atomics are
+// order-independent.
+__device__ __forceinline__ double fixed_point(double e, double scale) {
+    return __builtin_fma(e, scale, 4503599627370496.0) - 4503599627370496.0;
+}
+
+// Repetition penalty of one logit (Sampler.cs:31): s*rho if s < 0, else s/rho correctly rounded.
+// The quotient uses rinv = RN(1/rho) and one fma correction (Markstein): with s and rho in
+// [2^-60, 2^60] no intermediate leaves the normal range, so the result is the correctly rounded
+// s/rho; every other case (zeros, tiny or huge values, `fast` false) takes the IEEE division.
+__device__ __forceinline__ float penalize(float s, float rho, float rinv, bool fast) {
+    if (s < 0.0f) return s * rho;
+    if (!(fast && s >= 0x1p-60f && s <= 0x1p60f)) return s / rho;
+    const float t0 = s * rinv;
+    const float rem = __builtin_fmaf(-t0, rho, s);
+    return __builtin_fmaf(rem, rinv, t0);
+}
+
+// exp(d) for d <= 0 in fp32: 2^(d log2 e) with the product carried in two parts (the rounding
+// error of d*L2E recovered by fma, plus d times the tail of log2 e) and the hardware 2^x. Relative
+// error about 1e-7; 0 for d = -inf or results below 2^-126 (d is clamped at -256 first).
+__device__ __forceinline__ float exp_neg(float d) {
+    d = __builtin_fmaxf(d, -256.0f);
+    constexpr float kL2E = 1.44269502162933349609375f;          // fl32(log2 e)
+    constexpr float kL2ELo = 1.925963033500011079e-8f;          // log2 e - kL2E
+    constexpr float kLn2 = 0.693147180559945309f;
+    const float y = d * kL2E;
+    float yl = __builtin_fmaf(d, kL2E, -y);
+    yl = __builtin_fmaf(d, kL2ELo, yl);
+    const float e = __builtin_amdgcn_exp2f(y);
+    return __builtin_fmaf(e, yl * kLn2, e);
+}
+
+}  // namespace dev
+}  // namespace vxs

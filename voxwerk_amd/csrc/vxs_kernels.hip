@@ -1,517 +1,576 @@
 // vxs_kernels.hip — gfx950 kernels of the token sampler.
 //
-// Row-resident kernel: one 256-thread workgroup (4 wave64) owns one row of up to 8192 logits.
-// The row is read from HBM once, with 16-byte non-temporal loads in sweeps of 1024 elements
-// (thread t holds elements c*1024 + 4t + j), and stays in VGPRs for every step:
+// Row-resident sampler: one 256-thread workgroup (4 wave64) owns one row of up to 1024*NC logits
+// and keeps it in VGPRs from the single HBM read (16-byte non-temporal loads; thread t holds the
+// elements c*1024 + 4t + j) to the sampled id.
 //
-//   S1 penalty     distinct history ids via an LDS bitmap (atomicOr picks one owner per id);
-//                  the owner rescales the logit (true fp32 divide / multiply)  Sampler.cs:25-33
-//   S2 suppression [supp_begin, supp_end) except keep_id, then ban_id -> -inf TalkerGenerator.cs:247-248
-//   S3 greedy      first index of the max, no temperature                    Sampler.cs:37,90-95
-//   S4 temperature x * fl32(1/T)                                             Sampler.cs:39-40
-//   S5 top-k       k-th largest (ties kept) by a count-weighted bucket select Sampler.cs:42-49
-//   S6-S8          two regimes after top-k:
-//     exact        <= 256 candidates: candidates are compacted in index order and wave 0 runs the
-//                  reference's sequential fp64 arithmetic on them (softmax sum, stable (p, index)
-//                  order, cumulative top-p cut, renormalisation, index-order draw)  Sampler.cs:51-87
-//     parallel     more candidates (full-vocab nucleus): masses exp(x-m) as 2^-F fixed point
-//                  (exact, order-independent integer sums), top-p cut by a mass-weighted bucket
-//                  select over (d = x-m, index), draw by an index-order integer prefix search.
-//
-// Bucket select: level 1 spreads elements linearly over the value range (1024 LDS buckets),
-// refinement levels split the surviving key interval in the order-preserving u32 key space, and
-// the last <= 512 elements are ranked exactly. It finds the first element, in ascending
-// (key, index) order, at which the cumulative weight exceeds a target.
+//   S1 penalty      the row is staged in LDS; distinct history ids are found with an LDS bitmap
+//                   (atomicOr) and the first setter of each id rescales that logit in place
+//                   (fp32 s*rho, or the correctly rounded s/rho)                 Sampler.cs:25-33
+//   S2 suppression  [supp_begin, supp_end) except keep_id, then ban_id -> -inf   TalkerGenerator.cs:247-248
+//   S3 greedy       first index of the max, no temperature                       Sampler.cs:37,90-95
+//   S4 temperature  x * fl32(1/T)                                                Sampler.cs:39-40
+//   S5 top-k        k-th largest value (ties kept) by a count-weighted bucket select  Sampler.cs:42-49
+//   S6-S8, two regimes after top-k:
+//     exact      <= 256 candidates: compacted in index order; the reference's sequential fp64
+//                arithmetic runs on them (exp, index-order sum, stable (p, index) order, top-p
+//                cut, renormalisation, index-order draw)                          Sampler.cs:51-87
+//     nucleus    more candidates (full-vocabulary top-p): masses exp(x - max) are evaluated in
+//                fp32 (relative error ~2e-7) and rounded to multiples of 2^-F held in doubles, so
+//                every sum (histogram atomics, totals, prefixes) is exact and order-independent.
+//                One pass fills per-sweep LDS histograms over d = x - max; wave 0 scans them for
+//                the bucket where the ascending cumulative mass crosses (1 - top_p) * total and
+//                ranks that bucket's few elements by (d, index) for the exact cut; the sweep
+//                totals above the cut give the kept mass per sweep, so the index-order draw for
+//                floor(u * kept mass) only revisits the one sweep that contains it.
 //
 // Per-row errors are reported in out_ids[row] as negative VXS_ERR_* codes.
 #include <math.h>
 #include <stdint.h>
 
+#include "vxs_device.h"
 #include "vxs_internal.h"
 
 namespace vxs {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
-constexpr int kSweep = kThreads * 4;  // elements per float4 sweep of the workgroup
-constexpr int kBuckets = 1024;
-constexpr int kBucketsLog2 = 10;
-constexpr int kList = 512;     // elements ranked exactly at the end of a bucket select
-constexpr int kCandMax = 256;  // candidate count of the exact sequential regime
-constexpr float kNegInf = -__builtin_huge_valf();
-constexpr float kPosInf = __builtin_huge_valf();
+using namespace dev;
 
-typedef float f4 __attribute__((ext_vector_type(4)));
+constexpr int kT = 256;         // threads per row (one workgroup)
+constexpr int kWaves = kT / 64;
+constexpr int kSW = 4 * kT;     // elements per float4 sweep
+constexpr int kCandMax = 256;   // candidate count of the exact sequential regime
+constexpr int kLMax = 2 * kT;   // generic select: elements ranked exactly after bucketing
+constexpr int kNB = 1024;       // generic select: buckets (4 per thread)
+constexpr int kNBLog = 10;
+constexpr int kNLMax = 128;     // nucleus cut: crossing-bucket elements ranked by wave 0
 
-// ---- keys ------------------------------------------------------------------------------------
-// Order-preserving u32 image of a float; -0 maps to +0 because C# compares them equal.
-__device__ __forceinline__ uint32_t f2key(float f) {
-    if (f == 0.0f) f = 0.0f;
-    const uint32_t u = __float_as_uint(f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float key2f(uint32_t k) {
-    const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
-    return __uint_as_float(u);
-}
+template <int NC>
+struct Cfg {
+    static constexpr int NE = 4 * NC;   // elements per thread
+    static constexpr int VMAX = NC * kSW;
+    static constexpr int BMW = VMAX / 32;
+    static constexpr int NBP = NC <= 3 ? 1024 : (NC <= 6 ? 512 : 256);  // nucleus buckets per sweep
+    static constexpr int BPL = NBP / 64;                                // ... per lane of wave 0
+    static_assert(NE <= 64, "element masks are 64-bit");
+};
 
-// Round-to-nearest integer of e * 2^F for 0 <= e*2^F < 2^52, via the 2^52 magic constant.
-__device__ __forceinline__ uint64_t fixed_point(double e, double scale) {
-    const double t = __builtin_fma(e, scale, 4503599627370496.0);
-    return (uint64_t)__double_as_longlong(t) - 0x4330000000000000ull;
-}
+// Workgroup-combine sites: each is written once per row, so no trailing barrier is needed; the
+// refinement loop reuses its sites with an explicit barrier.
+enum Site : int {
+    kSiteErr,
+    kSiteNan,
+    kSiteArgV,
+    kSiteArgI,
+    kSiteStat0,  // + 4
+    kSiteFmin = kSiteStat0 + 4,
+    kSiteCnt2,
+    kSiteScanK,
+    kSiteLRankK,
+    kSiteLRankP,
+    kSiteScanP,
+    kSiteDraw,
+    kSiteLast,
+    kSitePSum,
+    kSiteRefine,
+    kSiteRefine2,
+    kSiteRefine3,
+    kSiteComp0,  // + NC
+    kSiteChunk0 = kSiteComp0 + 8,  // + NC
+    kSiteNScan0 = kSiteChunk0 + 8,  // + NC + 1
+    kSites = kSiteNScan0 + 9,
+};
 
-// ---- wave / workgroup primitives ----------------------------------------------------------
-template <typename T>
-__device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-__device__ __forceinline__ float wave_min(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-__device__ __forceinline__ uint32_t wave_umin(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, 64));
-    return v;
-}
-__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
-    return v;
-}
-__device__ __forceinline__ int wave_imax(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
-    return v;
-}
+struct Blk {
+    int lane, wv, t;
+    uint64_t (*slot)[4];
 
-// Workgroup-wide scratch for reductions and control values.
+    __device__ __forceinline__ void sync() const { __syncthreads(); }
+    // combine one wave-uniform 64-bit value per wave across the workgroup
+    template <class Op>
+    __device__ __forceinline__ uint64_t combine(uint64_t w, int site, Op op) const {
+        if (lane == 0) slot[site][wv] = w;
+        __syncthreads();
+        uint64_t r = slot[site][0];
+#pragma unroll
+        for (int i = 1; i < kWaves; i++) r = op(r, slot[site][i]);
+        return r;
+    }
+    __device__ __forceinline__ uint32_t sum(uint32_t x, int site) const {
+        return (uint32_t)combine(wave_sum(x), site, [](uint64_t p, uint64_t q) { return p + q; });
+    }
+    __device__ __forceinline__ uint32_t wsum_u(uint32_t w, int site) const {  // w wave-uniform
+        return (uint32_t)combine(w, site, [](uint64_t p, uint64_t q) { return p + q; });
+    }
+    __device__ __forceinline__ double dsum(double x, int site) const {
+        return __longlong_as_double((long long)combine((uint64_t)__double_as_longlong(wave_sum(x)), site,
+                                                       [](uint64_t p, uint64_t q) {
+                                                           return (uint64_t)__double_as_longlong(
+                                                               __longlong_as_double((long long)p) +
+                                                               __longlong_as_double((long long)q));
+                                                       }));
+    }
+    __device__ __forceinline__ float fmin_(float x, int site) const {
+        return __uint_as_float((uint32_t)combine(__float_as_uint(wave_min(x)), site, [](uint64_t p, uint64_t q) {
+            return (uint64_t)__float_as_uint(fminf(__uint_as_float((uint32_t)p), __uint_as_float((uint32_t)q)));
+        }));
+    }
+    __device__ __forceinline__ uint32_t umax(uint32_t x, int site) const {
+        return (uint32_t)combine(wave_umax(x), site, [](uint64_t p, uint64_t q) { return p > q ? p : q; });
+    }
+    __device__ __forceinline__ uint32_t umin(uint32_t x, int site) const {
+        return (uint32_t)combine(wave_umin(x), site, [](uint64_t p, uint64_t q) { return p < q ? p : q; });
+    }
+    __device__ __forceinline__ int imax(int x, int site) const {  // x >= -1
+        return (int)umax((uint32_t)(x + 1), site) - 1;
+    }
+    __device__ __forceinline__ bool any(bool p, int site) const {
+        return combine(wave_any(p) ? 1u : 0u, site, [](uint64_t a, uint64_t b) { return a | b; }) != 0;
+    }
+    // workgroup-wide exclusive prefix sums in thread order
+    __device__ __forceinline__ uint32_t excl_scan(uint32_t v, int site, uint32_t& total) const {
+        const uint32_t incl = wave_incl_sum(v);
+        if (lane == 0) slot[site][wv] = readlane(incl, 63);
+        __syncthreads();
+        uint32_t base = 0, tot = 0;
+#pragma unroll
+        for (int i = 0; i < kWaves; i++) {
+            const uint32_t s = (uint32_t)slot[site][i];
+            base += i < wv ? s : 0;
+            tot += s;
+        }
+        total = tot;
+        return base + incl - v;
+    }
+    __device__ __forceinline__ double excl_scan(double v, int site, double& total) const {
+        const double incl = wave_incl_sum(v);
+        if (lane == 0) slot[site][wv] = (uint64_t)__double_as_longlong(readlane_d(incl, 63));
+        __syncthreads();
+        double base = 0, tot = 0;
+#pragma unroll
+        for (int i = 0; i < kWaves; i++) {
+            const double s = __longlong_as_double((long long)slot[site][i]);
+            base += i < wv ? s : 0.0;
+            tot += s;
+        }
+        total = tot;
+        return base + incl - v;  // exact: integer-valued doubles below 2^53
+    }
+};
+
 struct Ctl {
-    uint64_t r64[kWaves * 8];
-    double rd[kWaves];
-    float rf[kWaves * 2];
-    uint32_t ru[kWaves * 4];
-    int32_t ri[kWaves * 2];
-    int32_t err;
     int32_t sel_b;
-    int32_t sel_idx;
-    uint32_t sel_key;
-    uint64_t sel_below;
-    int32_t found_idx;
     uint32_t list_n;
+    double sel_below;
+    uint32_t sel_key;
+    int32_t sel_idx;
+    double sel_cbelow;
+    int32_t found;
+    // nucleus cut (written by wave 0)
+    double S, T, below;
+    int32_t bstar;
+    double kept[8];
 };
 
-template <typename T>
-__device__ __forceinline__ T block_sum(T v, T* scratch) {
-    v = wave_sum(v);
-    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
-    __syncthreads();
-    T r = scratch[0];
-#pragma unroll
-    for (int i = 1; i < kWaves; i++) r += scratch[i];
-    __syncthreads();
-    return r;
-}
-
-template <int N>
-__device__ __forceinline__ void block_sum_vec(uint64_t (&v)[N], uint64_t* scratch) {
-    static_assert(N <= 8, "scratch holds 8 values per wave");
-#pragma unroll
-    for (int c = 0; c < N; c++) v[c] = wave_sum(v[c]);
-    if ((threadIdx.x & 63) == 0)
-#pragma unroll
-        for (int c = 0; c < N; c++) scratch[(threadIdx.x >> 6) * 8 + c] = v[c];
-    __syncthreads();
-#pragma unroll
-    for (int c = 0; c < N; c++) {
-        uint64_t r = 0;
-#pragma unroll
-        for (int i = 0; i < kWaves; i++) r += scratch[i * 8 + c];
-        v[c] = r;
-    }
-    __syncthreads();
-}
-
-__device__ __forceinline__ uint32_t block_umin(uint32_t v, uint32_t* scratch) {
-    v = wave_umin(v);
-    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
-    __syncthreads();
-    uint32_t r = scratch[0];
-#pragma unroll
-    for (int i = 1; i < kWaves; i++) r = min(r, scratch[i]);
-    __syncthreads();
-    return r;
-}
-__device__ __forceinline__ uint32_t block_umax(uint32_t v, uint32_t* scratch) {
-    v = wave_umax(v);
-    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
-    __syncthreads();
-    uint32_t r = scratch[0];
-#pragma unroll
-    for (int i = 1; i < kWaves; i++) r = max(r, scratch[i]);
-    __syncthreads();
-    return r;
-}
-__device__ __forceinline__ int block_imax(int v, int32_t* scratch) {
-    v = wave_imax(v);
-    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
-    __syncthreads();
-    int r = scratch[0];
-#pragma unroll
-    for (int i = 1; i < kWaves; i++) r = max(r, scratch[i]);
-    __syncthreads();
-    return r;
-}
-
-// Exclusive prefix sum over the workgroup in thread order; `total` gets the full sum.
-template <typename T>
-__device__ __forceinline__ T block_excl_scan(T v, T* scratch, T& total) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    T x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const T y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
-    if (lane == 63) scratch[w] = x;
-    __syncthreads();
-    T base = 0;
-    total = 0;
-#pragma unroll
-    for (int i = 0; i < kWaves; i++) {
-        const T s = scratch[i];
-        if (i < w) base += s;
-        total += s;
-    }
-    __syncthreads();
-    return base + x - v;
-}
-
-// ---- shared memory -------------------------------------------------------------------------
 template <int NC>
-struct SmemPenalty {
-    uint32_t bm[NC * kSweep / 32];
-    float pen[NC * kSweep];
-};
-struct SmemSelect {
-    uint64_t hist[kBuckets];
-    uint32_t lkey[kList];
-    int32_t lidx[kList];
-    uint64_t lw[kList];
-    int16_t lsorted[kList];
-};
-struct SmemExact {
-    float cx[kCandMax];
-    int32_t ci[kCandMax];
-    double cp[kCandMax];
-    int32_t csorted[kCandMax];
-};
-template <int NC>
-union Smem {
-    SmemPenalty<NC> pen;
-    SmemSelect sel;
-    SmemExact ex;
+struct RowSmem {
+    using C = Cfg<NC>;
+    uint32_t bm[C::BMW];
+    union {
+        float xs[C::VMAX];  // staged row for the penalty
+        struct {
+            double hist[kNB];
+            uint32_t lkey[kLMax];
+            int32_t lidx[kLMax];
+            double lw[kLMax];
+            double lws[kLMax];   // weights in rank order
+            int16_t lat[kLMax];  // list entry at each rank
+        } sel;
+        double nh[NC][C::NBP];  // nucleus histograms, one per sweep
+        struct {
+            float cx[kCandMax];
+            int32_t ci[kCandMax];
+            double cp[kCandMax];
+            int16_t cs[kCandMax];
+        } ex;
+    } u;
+    struct {
+        uint32_t key[kNLMax];
+        int32_t idx[kNLMax];
+        double w[kNLMax];
+        double ws[kNLMax];
+        int16_t at[kNLMax];
+    } nl;
+    Ctl ctl;
+    uint64_t slot[kSites][4];
 };
 
-// Element index of register slot e = c*4 + j.
-__device__ __forceinline__ int elem_index(int e) { return (e >> 2) * kSweep + (int)threadIdx.x * 4 + (e & 3); }
+// First element, in ascending (key, index) order over the `act` elements, at which the inclusive
+// cumulative weight exceeds T (weights and T are integer-valued doubles below 2^53); `sel.hist`
+// must be zero on entry. Returns key, index (only if need_idx) and the cumulative weight strictly
+// before the element. When the total weight is <= T the last element is returned. Level 1 spreads
+// the elements over kNB buckets with `b1` (monotone in key); a bucket with more than kLMax elements
+// is split in the u32 key space until few elements or a single key remain; the survivors are ranked
+// exactly.
+template <int NC, class KeyF, class WtF, class B1F>
+__device__ __forceinline__ void block_select(const Blk& g, RowSmem<NC>& sm, uint64_t act, double T, bool need_idx,
+                                             KeyF key, WtF wt, B1F b1, int scan_site, int rank_site,
+                                             uint32_t& okey, int& oidx, double& obelow) {
+    constexpr int NE = Cfg<NC>::NE;
+    auto& s = sm.u.sel;
+    auto eidx = [&](int e) { return (e >> 2) * kSW + g.t * 4 + (e & 3); };
 
-// Finds the first element, in ascending (key, index) order over the elements whose bit is set in
-// `active`, at which the inclusive cumulative weight exceeds T. Returns its key and index (index
-// only when need_idx). When the total weight is <= T the result is the last active element.
-// `b1(e)` is the level-1 bucket of slot e: monotone non-decreasing in key, in [0, kBuckets).
-template <int NC, class B1>
-__device__ void weighted_select(const uint32_t (&key)[NC * 4], const uint64_t (&w)[NC * 4], uint32_t active,
-                                uint64_t T, bool need_idx, B1 b1, SmemSelect& s, Ctl& ctl, uint32_t& out_key,
-                                int& out_idx) {
-    constexpr int NE = NC * 4;
-    const int tid = threadIdx.x;
-
-    // ---- level 1: linear buckets over the value range
-    for (int b = tid; b < kBuckets; b += kThreads) s.hist[b] = 0;
-    if (tid == 0) ctl.sel_b = -1;
-    __syncthreads();
 #pragma unroll
     for (int e = 0; e < NE; e++)
-        if ((active >> e) & 1u) atomicAdd((unsigned long long*)&s.hist[b1(e)], (unsigned long long)w[e]);
-    __syncthreads();
-    uint64_t below;
+        if ((act >> e) & 1u) atomicAdd(&s.hist[b1(e)], wt(e));
+    if (g.t == 0) {
+        sm.ctl.sel_b = -1;
+        sm.ctl.list_n = 0;
+    }
+    g.sync();
+    double below;
+    int bstar;
     {
-        uint64_t h[4];
+        double h[4];
+        double tot = 0.0;
 #pragma unroll
-        for (int j = 0; j < 4; j++) h[j] = s.hist[tid * 4 + j];
-        const uint64_t tot = h[0] + h[1] + h[2] + h[3];
-        uint64_t all;
-        const uint64_t excl = block_excl_scan(tot, ctl.r64, all);
+        for (int j = 0; j < 4; j++) {
+            h[j] = s.hist[g.t * 4 + j];
+            tot += h[j];
+        }
+        double all;
+        const double excl = g.excl_scan(tot, scan_site, all);
+        if (all <= T) {  // no crossing: the last element in (key, index) order
+            uint32_t km = 0;
+#pragma unroll
+            for (int e = 0; e < NE; e++)
+                if ((act >> e) & 1u) km = max(km, key(e));
+            km = g.umax(km, kSiteRefine);
+            g.sync();
+            int im = -1;
+#pragma unroll
+            for (int e = 0; e < NE; e++)
+                if (((act >> e) & 1u) && key(e) == km) im = max(im, eidx(e));
+            im = g.imax(im, kSiteRefine2);
+            g.sync();
+            double wl = 0.0;
+#pragma unroll
+            for (int e = 0; e < NE; e++)
+                if (((act >> e) & 1u) && eidx(e) == im) wl = wt(e);
+            wl = g.dsum(wl, kSiteRefine3);
+            g.sync();
+            okey = km;
+            oidx = im;
+            obelow = all - wl;
+            return;
+        }
         if (excl <= T && T - excl < tot) {
-            uint64_t run = excl;
+            double run = excl;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 if (T - run < h[j]) {
-                    ctl.sel_b = tid * 4 + j;
-                    ctl.sel_below = run;
+                    sm.ctl.sel_b = g.t * 4 + j;
+                    sm.ctl.sel_below = run;
                     break;
                 }
                 run += h[j];
             }
         }
-        __syncthreads();
-        if (ctl.sel_b < 0) {  // total weight <= T: the last active element
-            uint32_t kmax = 0;
-#pragma unroll
-            for (int e = 0; e < NE; e++)
-                if ((active >> e) & 1u) kmax = max(kmax, key[e]);
-            kmax = block_umax(kmax, ctl.ru);
-            int imax = -1;
-#pragma unroll
-            for (int e = 0; e < NE; e++)
-                if (((active >> e) & 1u) && key[e] == kmax) imax = max(imax, elem_index(e));
-            imax = block_imax(imax, ctl.ri);
-            out_key = kmax;
-            out_idx = imax;
-            return;
-        }
-        below = ctl.sel_below;
+        g.sync();
+        bstar = sm.ctl.sel_b;
+        below = sm.ctl.sel_below;
     }
-    const int bstar = ctl.sel_b;
-    // active elements of the chosen bucket
-    uint32_t in = 0;
+    uint64_t in = 0;
 #pragma unroll
     for (int e = 0; e < NE; e++)
-        if (((active >> e) & 1u) && b1(e) == bstar) in |= 1u << e;
+        if (((act >> e) & 1u) && b1(e) == bstar) in |= 1ull << e;
 
-    uint32_t klo, khi, L;
-    {
-        uint32_t mn = 0xffffffffu, mx = 0;
-#pragma unroll
-        for (int e = 0; e < NE; e++)
-            if ((in >> e) & 1u) {
-                mn = min(mn, key[e]);
-                mx = max(mx, key[e]);
-            }
-        klo = block_umin(mn, ctl.ru);
-        khi = block_umax(mx, ctl.ru + kWaves);
-        L = block_sum((uint32_t)__builtin_popcount(in), ctl.ru + 2 * kWaves);
-    }
-
-    // ---- refinement in key space until few elements or a single key remain
-    while (L > (uint32_t)kList && klo != khi) {
-        const uint32_t range = khi - klo;
-        const int bits = 32 - __clz(range);
-        const int shift = bits > kBucketsLog2 ? bits - kBucketsLog2 : 0;
-        for (int b = tid; b < kBuckets; b += kThreads) s.hist[b] = 0;
-        if (tid == 0) ctl.sel_b = -1;
-        __syncthreads();
-#pragma unroll
-        for (int e = 0; e < NE; e++)
-            if ((in >> e) & 1u) atomicAdd((unsigned long long*)&s.hist[(key[e] - klo) >> shift], (unsigned long long)w[e]);
-        __syncthreads();
-        const uint64_t T2 = T - below;
-        uint64_t h[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) h[j] = s.hist[tid * 4 + j];
-        const uint64_t tot = h[0] + h[1] + h[2] + h[3];
-        uint64_t all;
-        const uint64_t excl = block_excl_scan(tot, ctl.r64, all);
-        if (excl <= T2 && T2 - excl < tot) {
-            uint64_t run = excl;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                if (T2 - run < h[j]) {
-                    ctl.sel_b = tid * 4 + j;
-                    ctl.sel_below = run;
-                    break;
-                }
-                run += h[j];
-            }
-        }
-        __syncthreads();
-        const int b2 = ctl.sel_b;  // always found: the interval holds the crossing element
-        below += ctl.sel_below;
-        const uint64_t lo2 = (uint64_t)klo + ((uint64_t)b2 << shift);
-        const uint64_t hi2 = min((uint64_t)khi, lo2 + ((1ull << shift) - 1));
-        uint32_t in2 = 0, mn = 0xffffffffu, mx = 0;
-#pragma unroll
-        for (int e = 0; e < NE; e++)
-            if (((in >> e) & 1u) && key[e] >= lo2 && key[e] <= hi2) {
-                in2 |= 1u << e;
-                mn = min(mn, key[e]);
-                mx = max(mx, key[e]);
-            }
-        in = in2;
-        klo = block_umin(mn, ctl.ru);
-        khi = block_umax(mx, ctl.ru + kWaves);
-        L = block_sum((uint32_t)__builtin_popcount(in), ctl.ru + 2 * kWaves);
-    }
-
-    if (klo == khi) {  // a single key remains: ties, ordered by index
-        out_key = klo;
-        out_idx = -1;
-        if (!need_idx) return;
-        // every tied element has the same (non-zero) weight: take it from any holder
-        uint64_t mine = 0;
-#pragma unroll
-        for (int e = 0; e < NE; e++)
-            if ((in >> e) & 1u) mine = w[e];
-        const uint32_t whi = block_umax((uint32_t)(mine >> 32), ctl.ru);
-        const uint32_t wlo = block_umax((uint32_t)mine, ctl.ru + kWaves);
-        const uint64_t wt = ((uint64_t)whi << 32) | wlo;
-        const uint64_t nth = (T - below) / wt;  // 0-based position among the ties, index order
-        // locate the nth tied element in index order, sweep by sweep
-        uint64_t base = 0;
-        if (tid == 0) ctl.found_idx = -1;
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
-            const uint32_t mine = (in >> (c * 4)) & 0xfu;
-            const uint64_t cnt = (uint64_t)__builtin_popcount(mine);
-            uint64_t total;
-            const uint64_t excl = block_excl_scan(cnt, ctl.r64, total);
-            if (nth >= base + excl && nth < base + excl + cnt) {
-                uint64_t k = nth - base - excl;
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    if ((mine >> j) & 1u) {
-                        if (k == 0) {
-                            ctl.found_idx = c * kSweep + tid * 4 + j;
-                            break;
-                        }
-                        k--;
-                    }
-            }
-            base += total;
-        }
-        __syncthreads();
-        out_idx = ctl.found_idx;
-        return;
-    }
-
-    // ---- at most kList elements remain: rank them exactly by (key, index)
-    if (tid == 0) ctl.list_n = 0;
-    __syncthreads();
+    // gather the bucket's elements (slots beyond kLMax are only counted)
 #pragma unroll
     for (int e = 0; e < NE; e++)
         if ((in >> e) & 1u) {
-            const uint32_t slot = atomicAdd(&ctl.list_n, 1u);
-            s.lkey[slot] = key[e];
-            s.lidx[slot] = elem_index(e);
-            s.lw[slot] = w[e];
+            const uint32_t k = atomicAdd(&sm.ctl.list_n, 1u);
+            if (k < (uint32_t)kLMax) {
+                s.lkey[k] = key(e);
+                s.lidx[k] = eidx(e);
+                s.lw[k] = wt(e);
+            }
         }
-    __syncthreads();
-    const int n = (int)ctl.list_n;
-    for (int a = tid; a < n; a += kThreads) {
+    g.sync();
+    uint32_t n = sm.ctl.list_n;
+
+    if (n > (uint32_t)kLMax) {
+        // ---- crowded bucket: split its key interval until <= kLMax elements or a single key remain
+        uint32_t klo, khi;
+        {
+            uint32_t mn = 0xffffffffu, mx = 0;
+#pragma unroll
+            for (int e = 0; e < NE; e++)
+                if ((in >> e) & 1u) {
+                    mn = min(mn, key(e));
+                    mx = max(mx, key(e));
+                }
+            klo = g.umin(mn, kSiteRefine);
+            khi = g.umax(mx, kSiteRefine2);
+            g.sync();
+        }
+        while (n > (uint32_t)kLMax && klo != khi) {
+            const uint32_t range = khi - klo;
+            const int bits = 32 - __clz(range);
+            const int shift = bits > kNBLog ? bits - kNBLog : 0;
+            for (int b = g.t; b < kNB; b += kT) s.hist[b] = 0.0;
+            if (g.t == 0) sm.ctl.sel_b = -1;
+            g.sync();
+#pragma unroll
+            for (int e = 0; e < NE; e++)
+                if ((in >> e) & 1u) atomicAdd(&s.hist[(key(e) - klo) >> shift], wt(e));
+            g.sync();
+            const double T2 = T - below;
+            double h[4];
+            double tot = 0.0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                h[j] = s.hist[g.t * 4 + j];
+                tot += h[j];
+            }
+            double all;
+            const double excl = g.excl_scan(tot, kSiteRefine, all);
+            if (excl <= T2 && T2 - excl < tot) {
+                double run = excl;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    if (T2 - run < h[j]) {
+                        sm.ctl.sel_b = g.t * 4 + j;
+                        sm.ctl.sel_below = run;
+                        break;
+                    }
+                    run += h[j];
+                }
+            }
+            g.sync();
+            const int b2 = sm.ctl.sel_b;
+            below += sm.ctl.sel_below;
+            const uint64_t lo2 = (uint64_t)klo + ((uint64_t)b2 << shift);
+            const uint64_t hi2 = min((uint64_t)khi, lo2 + ((1ull << shift) - 1));
+            uint64_t in2 = 0;
+            uint32_t mn = 0xffffffffu, mx = 0, cnt = 0;
+#pragma unroll
+            for (int e = 0; e < NE; e++)
+                if (((in >> e) & 1u) && key(e) >= lo2 && key(e) <= hi2) {
+                    in2 |= 1ull << e;
+                    mn = min(mn, key(e));
+                    mx = max(mx, key(e));
+                    cnt++;
+                }
+            in = in2;
+            klo = g.umin(mn, kSiteRefine2);
+            khi = g.umax(mx, kSiteRefine3);
+            g.sync();
+            n = g.sum(cnt, kSiteRefine);
+            g.sync();
+        }
+        if (klo == khi && n > (uint32_t)kLMax) {
+            // ties: every remaining element has key klo and the same weight; order is by index
+            okey = klo;
+            oidx = -1;
+            double mine = 0.0;
+#pragma unroll
+            for (int e = 0; e < NE; e++)
+                if ((in >> e) & 1u) mine = wt(e);
+            const uint64_t mb = (uint64_t)__double_as_longlong(mine);  // non-negative: bits order as values
+            const uint64_t wb = ((uint64_t)g.umax((uint32_t)(mb >> 32), kSiteRefine) << 32) |
+                                g.umax((uint32_t)mb, kSiteRefine2);
+            g.sync();
+            const double wtie = __longlong_as_double((long long)wb);
+            if (!need_idx) {
+                obelow = below;
+                return;
+            }
+            const uint64_t nth = (uint64_t)(T - below) / (uint64_t)wtie;
+            obelow = below + (double)nth * wtie;
+            uint32_t base = 0;
+            if (g.t == 0) sm.ctl.found = -1;
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const uint32_t mine4 = (uint32_t)(in >> (c * 4)) & 0xfu;
+                const uint32_t cnt = (uint32_t)__builtin_popcount(mine4);
+                uint32_t total;
+                const uint32_t excl = g.excl_scan(cnt, kSiteRefine3, total);
+                if (nth >= (uint64_t)base + excl && nth < (uint64_t)base + excl + cnt) {
+                    uint64_t k = nth - base - excl;
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        if ((mine4 >> j) & 1u) {
+                            if (k == 0) {
+                                sm.ctl.found = c * kSW + g.t * 4 + j;
+                                break;
+                            }
+                            k--;
+                        }
+                }
+                base += total;
+                g.sync();
+            }
+            oidx = sm.ctl.found;
+            g.sync();
+            return;
+        }
+        // gather the (now small) interval
+        if (g.t == 0) sm.ctl.list_n = 0;
+        g.sync();
+#pragma unroll
+        for (int e = 0; e < NE; e++)
+            if ((in >> e) & 1u) {
+                const uint32_t k = atomicAdd(&sm.ctl.list_n, 1u);
+                s.lkey[k] = key(e);
+                s.lidx[k] = eidx(e);
+                s.lw[k] = wt(e);
+            }
+        g.sync();
+        n = sm.ctl.list_n;
+    }
+
+    // ---- rank the list by (key, index); thread t then owns ranks 2t and 2t+1
+    for (int a = g.t; a < (int)n; a += kT) {
         const uint32_t ka = s.lkey[a];
         const int ia = s.lidx[a];
         int rank = 0;
-        for (int b = 0; b < n; b++) {
+        for (int b = 0; b < (int)n; b++) {
             const uint32_t kb = s.lkey[b];
             rank += (kb < ka) || (kb == ka && s.lidx[b] < ia);
         }
-        s.lsorted[rank] = (int16_t)a;
+        s.lws[rank] = s.lw[a];
+        s.lat[rank] = (int16_t)a;
     }
-    __syncthreads();
-    if (tid == 0) {
-        uint64_t cum = below;
-        int pick = s.lsorted[n - 1];
-        for (int r = 0; r < n; r++) {
-            const int a = s.lsorted[r];
-            cum += s.lw[a];
-            if (cum > T) {
-                pick = a;
-                break;
-            }
+    if (g.t == 0) sm.ctl.sel_idx = -1;
+    g.sync();
+    const int r0 = 2 * g.t;
+    const double w0 = r0 < (int)n ? s.lws[r0] : 0.0;
+    const double w1 = r0 + 1 < (int)n ? s.lws[r0 + 1] : 0.0;
+    double tot;
+    const double ex = g.excl_scan(w0 + w1, rank_site, tot);
+    {
+        const double c0 = below + ex;  // cumulative weight before rank r0
+        int prank = -1;
+        double pbelow = 0.0;
+        if (r0 < (int)n && T >= c0 && T - c0 < w0) {
+            prank = r0;
+            pbelow = c0;
+        } else if (r0 + 1 < (int)n && T >= c0 + w0 && T - (c0 + w0) < w1) {
+            prank = r0 + 1;
+            pbelow = c0 + w0;
         }
-        ctl.sel_key = s.lkey[pick];
-        ctl.sel_idx = s.lidx[pick];
+        if (prank >= 0) {
+            const int at = s.lat[prank];
+            sm.ctl.sel_key = s.lkey[at];
+            sm.ctl.sel_idx = s.lidx[at];
+            sm.ctl.sel_cbelow = pbelow;
+        }
     }
-    __syncthreads();
-    out_key = ctl.sel_key;
-    out_idx = ctl.sel_idx;
-    __syncthreads();
+    g.sync();
+    okey = sm.ctl.sel_key;
+    oidx = sm.ctl.sel_idx;
+    obelow = sm.ctl.sel_cbelow;
+    g.sync();
 }
 
-// ---- the row-resident kernel ----------------------------------------------------------------
-template <int NC, bool VEC>
-__global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
-    constexpr int NE = NC * 4;
-    __shared__ Smem<NC> sm;
-    __shared__ Ctl ctl;
+// Occupancy target: 4 waves per SIMD where 128 VGPRs hold the row without spills.
+template <int NC>
+constexpr int kWavesPerEu = NC <= 3 ? 4 : 1;
 
-    const int tid = threadIdx.x;
+template <int NC>
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<NC>))) void sample_rows_kernel(
+    SampleArgs a, int vec) {
+    using C = Cfg<NC>;
+    constexpr int NE = C::NE;
+    __shared__ RowSmem<NC> sm;
+
+    Blk g;
+    g.lane = threadIdx.x & 63;
+    g.wv = threadIdx.x >> 6;
+    g.t = threadIdx.x;
+    g.slot = sm.slot;
     const int r = blockIdx.x;
+    auto eidx = [&](int e) { return (e >> 2) * kSW + g.t * 4 + (e & 3); };
+
     const int V = a.vocab;
     const vxs_params P = a.params[(int64_t)r * a.params_stride];
     const float* __restrict__ xrow = a.logits + (int64_t)r * a.ld;
+    const bool pen_on = P.rep_penalty != 1.0f && a.hist_off != nullptr;
 
+    // ---- issue the history prefetch and the row loads together
+    constexpr int HP = 2;  // ids per thread fetched up front (512 per row)
+    int h0 = 0, h1 = 0;
+    int pre[HP];
+    if (pen_on) {
+        h0 = a.hist_off[r];
+        h1 = a.hist_off[r + 1];
+#pragma unroll
+        for (int k = 0; k < HP; k++) {
+            const int h = h0 + g.t + k * kT;
+            pre[k] = h < h1 ? a.hist_ids[h] : 0;
+        }
+    }
     float v[NE];
 #pragma unroll
     for (int c = 0; c < NC; c++) {
-        const int i0 = c * kSweep + tid * 4;
-        if (VEC) {
-            if (i0 < V) {
-                const f4 q = __builtin_nontemporal_load((const f4*)(xrow + i0));
-                v[c * 4 + 0] = q.x;
-                v[c * 4 + 1] = q.y;
-                v[c * 4 + 2] = q.z;
-                v[c * 4 + 3] = q.w;
-            } else {
-#pragma unroll
-                for (int j = 0; j < 4; j++) v[c * 4 + j] = kNegInf;
-            }
+        const int i0 = c * kSW + g.t * 4;
+        if (vec && i0 + 3 < V) {
+            typedef float f4 __attribute__((ext_vector_type(4)));
+            const f4 q = __builtin_nontemporal_load((const f4*)(xrow + i0));
+            v[c * 4 + 0] = q.x;
+            v[c * 4 + 1] = q.y;
+            v[c * 4 + 2] = q.z;
+            v[c * 4 + 3] = q.w;
         } else {
 #pragma unroll
             for (int j = 0; j < 4; j++) v[c * 4 + j] = (i0 + j < V) ? xrow[i0 + j] : kNegInf;
         }
     }
-    uint32_t valid = 0;
-#pragma unroll
-    for (int e = 0; e < NE; e++)
-        if (elem_index(e) < V) valid |= 1u << e;
+    // entries past the vocabulary (pads of the last sweep) hold -inf: they never win, carry no mass
+    // and are never written back
 
     // ---- S1: repetition penalty over the distinct history ids
-    if (P.rep_penalty != 1.0f && a.hist_off != nullptr) {
-        const int h0 = a.hist_off[r], h1 = a.hist_off[r + 1];
-        if (h1 > h0) {
-            uint32_t* bm = sm.pen.bm;
-            float* pen = sm.pen.pen;
-            for (int w = tid; w < NC * kSweep / 32; w += kThreads) bm[w] = 0;
-            if (tid == 0) ctl.err = 0;
-            __syncthreads();
-            const float rho = P.rep_penalty;
-            for (int h = h0 + tid; h < h1; h += kThreads) {
-                const int id = a.hist_ids[h];
-                if ((unsigned)id >= (unsigned)V) {
-                    ctl.err = VXS_ERR_ID_OUT_OF_RANGE;
-                    continue;
-                }
-                const uint32_t bit = 1u << (id & 31);
-                const uint32_t old = atomicOr(&bm[id >> 5], bit);
-                if (!(old & bit)) {
-                    const float sv = xrow[id];
-                    pen[id] = sv < 0.0f ? sv * rho : sv / rho;
-                }
-            }
-            __syncthreads();
-            if (ctl.err != 0) {
-                if (tid == 0) a.out_ids[r] = ctl.err;
+    if (pen_on && h1 > h0) {
+        const float rho = P.rep_penalty;
+        const float rinv = 1.0f / rho;
+        const float arho = __builtin_fabsf(rho);
+        const bool fast = arho >= 0x1p-60f && arho <= 0x1p60f;
+        bool bad = false;
+        // The row is staged in LDS; the thread whose atomicOr first sets an id's bit owns the id and
+        // rescales that logit in place, then every thread reloads its elements.
+        float* xs = sm.u.xs;
+        typedef float f4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+            *(f4*)(xs + c * kSW + g.t * 4) = f4{v[c * 4 + 0], v[c * 4 + 1], v[c * 4 + 2], v[c * 4 + 3]};
+        for (int w = g.t; w < C::BMW; w += kT) sm.bm[w] = 0;
+        g.sync();
+        auto own = [&](int id) {
+            if ((unsigned)id >= (unsigned)V) {
+                bad = true;
                 return;
             }
+            const uint32_t bit = 1u << (id & 31);
+            if (!(atomicOr(&sm.bm[id >> 5], bit) & bit)) xs[id] = penalize(xs[id], rho, rinv, fast);
+        };
 #pragma unroll
-            for (int e = 0; e < NE; e++) {
-                const int i = elem_index(e);
-                if (((valid >> e) & 1u) && ((bm[i >> 5] >> (i & 31)) & 1u)) v[e] = pen[i];
-            }
-            __syncthreads();
+        for (int k = 0; k < HP; k++)
+            if (h0 + g.t + k * kT < h1) own(pre[k]);
+        for (int h = h0 + g.t + HP * kT; h < h1; h += kT) own(a.hist_ids[h]);
+        if (g.any(bad, kSiteErr)) {
+            if (g.t == 0) a.out_ids[r] = VXS_ERR_ID_OUT_OF_RANGE;
+            return;
         }
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const f4 q = *(const f4*)(xs + c * kSW + g.t * 4);
+            v[c * 4 + 0] = q.x;
+            v[c * 4 + 1] = q.y;
+            v[c * 4 + 2] = q.z;
+            v[c * 4 + 3] = q.w;
+        }
+        g.sync();  // LDS is reused below
     }
 
     float* orow = a.out_logits ? a.out_logits + (int64_t)r * V : nullptr;
@@ -520,21 +579,21 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
         if (!orow) return;
 #pragma unroll
         for (int e = 0; e < NE; e++)
-            if ((valid >> e) & 1u) orow[elem_index(e)] = v[e];
+            if (eidx(e) < V) orow[eidx(e)] = v[e];
     };
 
     if (a.kflags & KF_STOP_AFTER_PENALTY) {
         write_logits();
-        if (tid == 0) a.out_ids[r] = 0;
+        if (g.t == 0) a.out_ids[r] = 0;
         return;
     }
 
     // ---- S2: suppression
-    {
+    if (P.supp_begin < P.supp_end || P.ban_id >= 0) {
         const int sb = max(P.supp_begin, 0), se = min(P.supp_end, V);
 #pragma unroll
         for (int e = 0; e < NE; e++) {
-            const int i = elem_index(e);
+            const int i = eidx(e);
             if ((i >= sb && i < se && i != P.keep_id) || i == P.ban_id) v[e] = kNegInf;
         }
     }
@@ -546,141 +605,146 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
         bool nan = false;
 #pragma unroll
         for (int e = 0; e < NE; e++) {
-            if (!((valid >> e) & 1u)) continue;
-            const int i = elem_index(e);
             nan |= v[e] != v[e];
-            if (v[e] > bv || (v[e] == bv && i < bi)) {
+            if (v[e] > bv || (v[e] == bv && eidx(e) < bi)) {
                 bv = v[e];
-                bi = i;
+                bi = eidx(e);
             }
         }
+        wave_argmax(bv, bi);
+        if (g.lane == 0) {
+            g.slot[kSiteArgV][g.wv] = __float_as_uint(bv);
+            g.slot[kSiteArgI][g.wv] = (uint32_t)bi;
+        }
+        const bool anynan = g.any(nan, kSiteNan);  // its barrier also publishes the argmax slots
+        bv = __uint_as_float((uint32_t)g.slot[kSiteArgV][0]);
+        bi = (int)g.slot[kSiteArgI][0];
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
+        for (int i = 1; i < kWaves; i++) {
+            const float ov = __uint_as_float((uint32_t)g.slot[kSiteArgV][i]);
+            const int oi = (int)g.slot[kSiteArgI][i];
             if (ov > bv || (ov == bv && oi < bi)) {
                 bv = ov;
                 bi = oi;
             }
         }
-        const int lane = tid & 63, wid = tid >> 6;
-        if (lane == 0) {
-            ctl.rf[wid] = bv;
-            ctl.ri[wid] = bi;
-        }
-        const int anynan = block_sum((uint32_t)nan, ctl.ru + 3 * kWaves);
-        if (tid == 0) {
-            float gv = ctl.rf[0];
-            int gi = ctl.ri[0];
-            for (int i = 1; i < kWaves; i++)
-                if (ctl.rf[i] > gv || (ctl.rf[i] == gv && ctl.ri[i] < gi)) {
-                    gv = ctl.rf[i];
-                    gi = ctl.ri[i];
-                }
-            a.out_ids[r] = anynan ? VXS_ERR_NONFINITE : gi;
-        }
+        if (g.t == 0) a.out_ids[r] = anynan ? VXS_ERR_NONFINITE : bi;
         write_logits();
         if (prow)
 #pragma unroll
             for (int e = 0; e < NE; e++)
-                if ((valid >> e) & 1u) prow[elem_index(e)] = 0.0;
+                if (eidx(e) < V) prow[eidx(e)] = 0.0;
         return;
     }
 
     // ---- S4: temperature, and the finite-input contract
-    const float invT = 1.0f / P.temperature;
-    bool bad = false;
+    const float invT = P.temperature == 1.0f ? 1.0f : 1.0f / P.temperature;
+    if (invT != 1.0f) {
 #pragma unroll
-    for (int e = 0; e < NE; e++)
-        if ((valid >> e) & 1u) {
-            v[e] *= invT;
-            bad |= (v[e] != v[e]) || v[e] == kPosInf;
-        }
-    float mx = kNegInf, mn = kPosInf;
-    uint32_t cnt = 0;
+        for (int e = 0; e < NE; e++) v[e] *= invT;
+        if (!(invT > 0.0f))  // negative or NaN scale: pads go back to -inf
 #pragma unroll
-    for (int e = 0; e < NE; e++)
-        if (((valid >> e) & 1u) && v[e] != kNegInf) {
-            mx = fmaxf(mx, v[e]);
-            mn = fminf(mn, v[e]);
-            cnt++;
-        }
+            for (int e = 0; e < NE; e++)
+                if (eidx(e) >= V) v[e] = kNegInf;
+    }
+    const bool topp = P.top_p < 1.0f;
+    float mx, mn;  // max; min (including -inf entries)
+    uint32_t cnt;  // finite entries
     {
-        mx = wave_max(mx);
-        mn = wave_min(mn);
-        cnt = wave_sum(cnt);
-        uint32_t b = wave_sum((uint32_t)bad);
-        const int lane = tid & 63, wid = tid >> 6;
-        if (lane == 0) {
-            ctl.rf[wid] = mx;
-            ctl.rf[kWaves + wid] = mn;
-            ctl.ru[wid] = cnt;
-            ctl.ru[kWaves + wid] = b;
+        uint64_t badm = 0;
+        float tmx = kNegInf, tmn = kPosInf;
+#pragma unroll
+        for (int e = 0; e < NE; e++) {
+            badm |= __ballot((v[e] != v[e]) || v[e] == kPosInf);
+            tmx = fmaxf(tmx, v[e]);
+            tmn = fminf(tmn, v[e]);
         }
-        __syncthreads();
-        mx = ctl.rf[0];
-        mn = ctl.rf[kWaves];
-        cnt = ctl.ru[0];
-        b = ctl.ru[kWaves];
-        for (int i = 1; i < kWaves; i++) {
-            mx = fmaxf(mx, ctl.rf[i]);
-            mn = fminf(mn, ctl.rf[kWaves + i]);
-            cnt += ctl.ru[i];
-            b += ctl.ru[kWaves + i];
+        const float wmx = wave_fmax(tmx);
+        const float wmn = wave_fmin(tmn);
+        if (g.lane == 0) {
+            g.slot[kSiteStat0 + 0][g.wv] = __float_as_uint(wmx);
+            g.slot[kSiteStat0 + 1][g.wv] = __float_as_uint(wmn);
+            g.slot[kSiteStat0 + 3][g.wv] = badm != 0;
         }
-        __syncthreads();
-        if (b) {
-            if (tid == 0) a.out_ids[r] = VXS_ERR_NONFINITE;
+        // zero the nucleus histograms while the statistics are published
+        if (topp)
+            for (int b = g.t; b < NC * C::NBP; b += kT) (&sm.u.nh[0][0])[b] = 0.0;
+        g.sync();
+        mx = kNegInf;
+        mn = kPosInf;
+        uint64_t anybad = 0;
+#pragma unroll
+        for (int i = 0; i < kWaves; i++) {
+            mx = fmaxf(mx, __uint_as_float((uint32_t)g.slot[kSiteStat0 + 0][i]));
+            mn = fminf(mn, __uint_as_float((uint32_t)g.slot[kSiteStat0 + 1][i]));
+            anybad |= g.slot[kSiteStat0 + 3][i];
+        }
+        if (anybad) {
+            if (g.t == 0) a.out_ids[r] = VXS_ERR_NONFINITE;
             return;
+        }
+        cnt = (uint32_t)V;
+        if (mn == kNegInf) {  // some entries are -inf (suppressed, masked or pads): count the rest
+            uint32_t cntw = 0;
+#pragma unroll
+            for (int e = 0; e < NE; e++) cntw += (uint32_t)__builtin_popcountll(__ballot(v[e] != kNegInf));
+            cnt = g.wsum_u(cntw, kSiteStat0 + 2);
         }
     }
 
     // every entry is -inf: p = 0/0 everywhere and the reference's draw returns the last id
     if (cnt == 0) {
-        if (tid == 0) a.out_ids[r] = V - 1;
+        if (g.t == 0) a.out_ids[r] = V - 1;
         write_logits();
         if (prow)
 #pragma unroll
             for (int e = 0; e < NE; e++)
-                if ((valid >> e) & 1u) prow[elem_index(e)] = __builtin_nan("");
+                if (eidx(e) < V) prow[eidx(e)] = __builtin_nan("");
         return;
     }
 
     // ---- S5: top-k (ties at the k-th value are kept)
-    uint32_t key[NE];
-    uint64_t wgt[NE];
     const int K = P.top_k;
     if (K > 0 && K < V && (uint32_t)K < cnt) {
-        uint32_t act = 0;
-#pragma unroll
-        for (int e = 0; e < NE; e++) {
-            key[e] = f2key(v[e]);
-            wgt[e] = 1;
-            if (((valid >> e) & 1u) && v[e] != kNegInf) act |= 1u << e;
-        }
-        const double lo = (double)mn;
-        const double scale = mx > mn ? (double)kBuckets / ((double)mx - lo) : 0.0;
-        auto b1 = [&](int e) -> int {
-            const int b = (int)(((double)v[e] - lo) * scale);
-            return min(max(b, 0), kBuckets - 1);
-        };
-        uint32_t kkey;
-        int kidx;
-        weighted_select<NC>(key, wgt, act, (uint64_t)(cnt - (uint32_t)K), false, b1, sm.sel, ctl, kkey, kidx);
-        const float kth = key2f(kkey);
-        uint32_t c2 = 0;
-        float mn2 = kPosInf;
+        for (int b = g.t; b < kNB; b += kT) sm.u.sel.hist[b] = 0.0;
+        uint64_t act = 0;
+        float fmn = kPosInf;  // smallest finite value
 #pragma unroll
         for (int e = 0; e < NE; e++)
-            if ((valid >> e) & 1u) {
-                if (v[e] < kth) v[e] = kNegInf;
-                if (v[e] != kNegInf) {
-                    c2++;
-                    mn2 = fminf(mn2, v[e]);
-                }
+            if (v[e] != kNegInf) {
+                act |= 1ull << e;
+                fmn = fminf(fmn, v[e]);
             }
-        cnt = block_sum(c2, ctl.ru);
-        mn = kth;  // the smallest kept value
+        const float lo = g.fmin_(fmn, kSiteFmin);  // its barrier publishes the zeroed histogram
+        const float span = mx - lo;                // may round; any monotone bucket map is exact here
+        const float scale = (span > 0.0f && span < kPosInf) ? (float)kNB / span : 0.0f;
+        auto b1 = [&](int e) -> int {
+            float x = v[e];
+            asm volatile("" : "+v"(x));
+            return (int)fminf(fmaxf((x - lo) * scale, 0.0f), (float)(kNB - 1));
+        };
+        auto key = [&](int e) -> uint32_t {
+            float x = v[e];
+            asm volatile("" : "+v"(x));
+            return f2key(x);
+        };
+        auto wt = [&](int) -> double { return 1.0; };
+        uint32_t kkey;
+        int kidx;
+        double kbelow;
+        block_select<NC>(g, sm, act, (double)(cnt - (uint32_t)K), false, key, wt, b1, kSiteScanK, kSiteLRankK, kkey,
+                         kidx, kbelow);
+        const float kth = key2f(kkey);
+        uint32_t c2 = 0;
+#pragma unroll
+        for (int e = 0; e < NE; e++) {
+            if (v[e] < kth) v[e] = kNegInf;
+            c2 += (uint32_t)__builtin_popcountll(__ballot(v[e] != kNegInf));
+        }
+        if (topp)
+            for (int b = g.t; b < NC * C::NBP; b += kT) (&sm.u.nh[0][0])[b] = 0.0;
+        cnt = g.wsum_u(c2, kSiteCnt2);
+        mn = kth;  // every kept value is >= kth; masked entries are -inf and carry no mass
     }
     write_logits();
 
@@ -689,25 +753,22 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
 
     if (cnt <= (uint32_t)kCandMax) {
         // ================= exact regime: the reference's sequential fp64 arithmetic =================
-        SmemExact& ex = sm.ex;
-        // compact candidates in index order
+        auto& ex = sm.u.ex;
+        g.sync();
         uint32_t base = 0;
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             uint32_t mine = 0;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int e = c * 4 + j;
-                if (((valid >> e) & 1u) && v[e] != kNegInf) mine++;
-            }
+            for (int j = 0; j < 4; j++) mine += v[c * 4 + j] != kNegInf ? 1u : 0u;
             uint32_t total;
-            uint32_t off = base + block_excl_scan(mine, ctl.ru, total);
+            uint32_t off = base + g.excl_scan(mine, kSiteComp0 + c, total);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int e = c * 4 + j;
-                if (((valid >> e) & 1u) && v[e] != kNegInf) {
+                if (v[e] != kNegInf) {
                     ex.cx[off] = v[e];
-                    ex.ci[off] = elem_index(e);
+                    ex.ci[off] = eidx(e);
                     off++;
                 }
             }
@@ -716,31 +777,30 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
         if (prow)
 #pragma unroll
             for (int e = 0; e < NE; e++)
-                if (((valid >> e) & 1u) && v[e] == kNegInf) prow[elem_index(e)] = 0.0;
-        __syncthreads();
-        // Parallel phases stride the candidates over the workgroup; sequential phases are run
-        // redundantly by every thread on LDS broadcast reads, so each yields a uniform value.
+                if (eidx(e) < V && v[e] == kNegInf) prow[eidx(e)] = 0.0;
+        g.sync();
+        // Parallel phases stride the candidates over the workgroup; sequential phases run
+        // redundantly in every thread on LDS broadcast reads, so each yields a uniform value.
         const int n = (int)cnt;
-        // e_i = exp((double)fl32(x_i - max))                                  Sampler.cs:57
-        for (int j = tid; j < n; j += kThreads) ex.cp[j] = exp((double)(ex.cx[j] - m));
-        __syncthreads();
-        double sum = 0.0;  // sequential in index order                                 :58
+        for (int j = g.t; j < n; j += kT) ex.cp[j] = exp((double)(ex.cx[j] - m));  // Sampler.cs:57
+        g.sync();
+        double sum = 0.0;  // sequential in index order                                  :58
         for (int j = 0; j < n; j++) sum += ex.cp[j];
-        __syncthreads();
-        for (int j = tid; j < n; j += kThreads) ex.cp[j] = ex.cp[j] / sum;  //          :60
-        __syncthreads();
-        if (P.top_p < 1.0f) {  //                                                      :62-75
-            // stable ascending (p, index) order of the candidates (index order == slot order)
-            for (int j = tid; j < n; j += kThreads) {
+        g.sync();
+        for (int j = g.t; j < n; j += kT) ex.cp[j] = ex.cp[j] / sum;  //                 :60
+        g.sync();
+        if (topp) {  //                                                                 :62-75
+            // stable ascending (p, index) order of the candidates (slot order == index order)
+            for (int j = g.t; j < n; j += kT) {
                 const double pj = ex.cp[j];
                 int rank = 0;
                 for (int l = 0; l < n; l++) {
                     const double pl = ex.cp[l];
                     rank += (pl < pj) || (pl == pj && l < j);
                 }
-                ex.csorted[rank] = j;
+                ex.cs[rank] = (int16_t)j;
             }
-            __syncthreads();
+            g.sync();
             const double thr = (double)(1.0f - P.top_p);
             double cum = 0.0;
             // The largest (p, index) entry is the reference's last sorted position, which its
@@ -748,22 +808,22 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
             // nothing. The scan only reads; the removed prefix is zeroed after a barrier.
             int nrem = n - 1;
             for (int s = 0; s < n - 1; s++) {
-                cum += ex.cp[ex.csorted[s]];
+                cum += ex.cp[ex.cs[s]];
                 if (!(cum <= thr)) {
                     nrem = s;
                     break;
                 }
             }
-            __syncthreads();
-            for (int s = tid; s < nrem; s += kThreads) ex.cp[ex.csorted[s]] = 0.0;
-            __syncthreads();
+            g.sync();
+            for (int s = g.t; s < nrem; s += kT) ex.cp[ex.cs[s]] = 0.0;
+            g.sync();
             double s2 = 0.0;  // probs.Sum(), sequential
             for (int j = 0; j < n; j++) s2 += ex.cp[j];
-            __syncthreads();
-            for (int j = tid; j < n; j += kThreads) ex.cp[j] = ex.cp[j] / s2;
-            __syncthreads();
+            g.sync();
+            for (int j = g.t; j < n; j += kT) ex.cp[j] = ex.cp[j] / s2;
+            g.sync();
         }
-        // inverse-CDF draw in index order                                              :77-87
+        // inverse-CDF draw in index order                                               :77-87
         double acc = 0.0;
         int last = 0, pick = -1;
         for (int j = 0; j < n; j++) {
@@ -776,137 +836,322 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
                 break;
             }
         }
-        if (tid == 0) a.out_ids[r] = pick >= 0 ? pick : last;
+        if (g.t == 0) a.out_ids[r] = pick >= 0 ? pick : last;
         if (prow)
-            for (int j = tid; j < n; j += kThreads) prow[ex.ci[j]] = ex.cp[j];
+            for (int j = g.t; j < n; j += kT) prow[ex.ci[j]] = ex.cp[j];
         return;
     }
 
-    // ================= parallel regime: fixed-point masses, bucket-selected nucleus =================
-    // F fraction bits so that vocab * 2^F < 2^62 and e * 2^F < 2^52.
-    const int F = min(51, 62 - (32 - __clz(V - 1)));
+    // =========== nucleus regime: exact fixed-point masses, histogram-located top-p cut ===========
+    // F fraction bits: vocab * 2^F <= 2^53 (exact double sums) and e * 2^F < 2^52.
+    const int F = min(51, 53 - (32 - __clz(V - 1)));
     const double scaleF = __builtin_ldexp(1.0, F);
-    uint32_t member = 0, positive = 0;
-    uint64_t sq = 0;
 #pragma unroll
-    for (int e = 0; e < NE; e++) {
-        wgt[e] = 0;
-        key[e] = 0;
-        if (((valid >> e) & 1u) && v[e] != kNegInf) {
-            const float d = v[e] - m;
-            const double ee = exp((double)d);
-            key[e] = f2key(d);
-            wgt[e] = fixed_point(ee, scaleF);
-            member |= 1u << e;
-            if (ee > 0.0) positive |= 1u << e;
-            sq += wgt[e];
-        }
-    }
-    const uint64_t S = block_sum(sq, ctl.r64);
-    uint32_t kept = member;
-    if (P.top_p < 1.0f) {
-        const double thr = (double)(1.0f - P.top_p);
-        const uint64_t T = thr >= 1.0 ? ~0ull : (uint64_t)(thr * (double)S);
-        const float dmin = mn - m;
-        const double lo = fmax((double)dmin, -64.0);
-        const double scale = lo < 0.0 ? (double)kBuckets / (-lo) : 0.0;
-        auto b1 = [&](int e) -> int {
-            const int b = (int)(((double)key2f(key[e]) - lo) * scale);
-            return min(max(b, 0), kBuckets - 1);
+    for (int e = 0; e < NE; e++) v[e] = v[e] - m;  // d = x - max; -inf stays -inf
+    // Masses and keys are recomputed where they are needed (a few VALU ops) instead of being kept
+    // live; the empty asm stops the compiler from caching them in VGPRs.
+    auto qof = [&](int e) -> double {
+        float x = v[e];
+        asm volatile("" : "+v"(x));
+        return fixed_point((double)exp_neg(x), scaleF);
+    };
+    auto keyof = [&](int e) -> uint32_t {
+        float x = v[e];
+        asm volatile("" : "+v"(x));
+        return f2key(x);
+    };
+    float dc = kNegInf;  // cut: keep d > dc, or d == dc with index >= ic
+    int ic = 0x7fffffff;
+    auto kept = [&](int e) { return v[e] > dc || (v[e] == dc && eidx(e) >= ic); };
+    double S = 0.0, Skept = 0.0;
+    double kc[NC];  // kept mass per sweep (uniform)
+    if (topp) {
+        constexpr int NBP = C::NBP, BPT = NBP / kT;
+        // buckets linear in d over [lo, 0]; lo is the row minimum, or -64 when lower
+        const float lo = fmaxf(mn - m, -64.0f);
+        const float scale = lo < -1e-30f ? (float)NBP / -lo : 0.0f;
+        const float off = -lo * scale;
+        auto bk = [&](int e) -> int {
+            float x = v[e];
+            asm volatile("" : "+v"(x));
+            return (int)__builtin_amdgcn_fmed3f(__builtin_fmaf(x, scale, off), 0.0f, (float)(NBP - 1));
         };
-        uint32_t ckey;
-        int cidx;
-        weighted_select<NC>(key, wgt, member, T, true, b1, sm.sel, ctl, ckey, cidx);
-        kept = 0;
 #pragma unroll
-        for (int e = 0; e < NE; e++)
-            if (((member >> e) & 1u) && (key[e] > ckey || (key[e] == ckey && elem_index(e) >= cidx)))
-                kept |= 1u << e;
-    }
-    // draw: first kept index (index order) whose inclusive prefix mass exceeds floor(u * S_kept)
-    uint64_t cs[NC];
-#pragma unroll
-    for (int c = 0; c < NC; c++) {
-        cs[c] = 0;
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            if ((kept >> (c * 4 + j)) & 1u) cs[c] += wgt[c * 4 + j];
-    }
-    uint64_t ct[NC];
-#pragma unroll
-    for (int c = 0; c < NC; c++) ct[c] = cs[c];
-    block_sum_vec<NC>(ct, ctl.r64);
-    uint64_t Skept = 0;
-#pragma unroll
-    for (int c = 0; c < NC; c++) Skept += ct[c];
-    const uint64_t D = (uint64_t)(u * (double)Skept);
-    int cstar = -1;
-    uint64_t run = 0;
-#pragma unroll
-    for (int c = 0; c < NC; c++) {
-        if (cstar < 0) {
-            if (D - run < ct[c] && D >= run) cstar = c;
-            else run += ct[c];
+        for (int e = 0; e < NE; e++)  // -inf entries add 0 to bucket 0
+            atomicAdd(&sm.u.nh[e >> 2][bk(e)], fixed_point((double)exp_neg(v[e]), scaleF));
+        if (g.t == 0) {
+            sm.ctl.bstar = -1;
+            sm.ctl.list_n = 0;
         }
+        g.sync();
+        // Thread t owns buckets [t*BPT, (t+1)*BPT) of every sweep. One combined exclusive scan over
+        // threads of (all sweeps, each sweep) gives the total S, the crossing bucket and, per sweep,
+        // the mass of the buckets above it.
+        double hs[NC + 1];
+        hs[0] = 0.0;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            double lt = 0.0;
+#pragma unroll
+            for (int j = 0; j < BPT; j++) lt += sm.u.nh[c][g.t * BPT + j];
+            hs[c + 1] = lt;
+            hs[0] += lt;
+        }
+        double incl[NC + 1];
+#pragma unroll
+        for (int i = 0; i <= NC; i++) {
+            incl[i] = wave_incl_sum(hs[i]);
+            if (g.lane == 0) g.slot[kSiteNScan0 + i][g.wv] = (uint64_t)__double_as_longlong(readlane_d(incl[i], 63));
+        }
+        g.sync();
+        double exs[NC + 1], tts[NC + 1];
+#pragma unroll
+        for (int i = 0; i <= NC; i++) {
+            double base = 0.0, tt = 0.0;
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) {
+                const double sv = __longlong_as_double((long long)g.slot[kSiteNScan0 + i][w]);
+                base += w < g.wv ? sv : 0.0;
+                tt += sv;
+            }
+            exs[i] = base + incl[i] - hs[i];
+            tts[i] = tt;
+        }
+        S = tts[0];
+        const double thr = (double)(1.0f - P.top_p);
+        const double T = thr >= 1.0 ? 1e300 : floor(thr * S);
+        if (exs[0] <= T && T - exs[0] < hs[0]) {  // this thread holds the crossing bucket
+            double run = exs[0];
+            double pre[NC];
+#pragma unroll
+            for (int c = 0; c < NC; c++) pre[c] = exs[c + 1];
+#pragma unroll
+            for (int j = 0; j < BPT; j++) {
+                double hb = 0.0;
+#pragma unroll
+                for (int c = 0; c < NC; c++) hb += sm.u.nh[c][g.t * BPT + j];
+                if (T - run < hb) {
+                    sm.ctl.bstar = g.t * BPT + j;
+                    sm.ctl.below = run;
+#pragma unroll
+                    for (int c = 0; c < NC; c++)  // sweep mass above the crossing bucket
+                        sm.ctl.kept[c] = tts[c + 1] - (pre[c] + sm.u.nh[c][g.t * BPT + j]);
+                    break;
+                }
+                run += hb;
+#pragma unroll
+                for (int c = 0; c < NC; c++) pre[c] += sm.u.nh[c][g.t * BPT + j];
+            }
+        }
+        g.sync();
+        const int bstar = sm.ctl.bstar;
+        double cbelow = 0.0;
+        bool fast = bstar >= 0;
+        if (fast) {
+            const double below = sm.ctl.below;
+            // gather the crossing bucket
+#pragma unroll
+            for (int e = 0; e < NE; e++)
+                if (v[e] != kNegInf && bk(e) == bstar) {
+                    const uint32_t k = atomicAdd(&sm.ctl.list_n, 1u);
+                    if (k < (uint32_t)kNLMax) {
+                        sm.nl.key[k] = keyof(e);
+                        sm.nl.idx[k] = eidx(e);
+                        sm.nl.w[k] = qof(e);
+                    }
+                }
+            g.sync();
+            const int n = (int)sm.ctl.list_n;
+            fast = n <= kNLMax;
+            if (fast) {
+                if (g.wv == 0) {
+                    // rank by (key, index) in wave 0: lane l holds list entries l and l+64 in
+                    // registers and compares them with every entry broadcast by readlane; lane l
+                    // then owns ranks 2l and 2l+1
+                    const int lane = g.lane;
+                    const uint32_t ka0 = lane < n ? sm.nl.key[lane] : 0xffffffffu;
+                    const int ia0 = lane < n ? sm.nl.idx[lane] : 0x7fffffff;
+                    const uint32_t ka1 = lane + 64 < n ? sm.nl.key[lane + 64] : 0xffffffffu;
+                    const int ia1 = lane + 64 < n ? sm.nl.idx[lane + 64] : 0x7fffffff;
+                    int rk0 = 0, rk1 = 0;
+                    const int n0 = min(n, 64);
+                    for (int b = 0; b < n0; b++) {
+                        const uint32_t kb = readlane(ka0, b);
+                        const int ib = (int)readlane((uint32_t)ia0, b);
+                        rk0 += (kb < ka0) || (kb == ka0 && ib < ia0);
+                        rk1 += (kb < ka1) || (kb == ka1 && ib < ia1);
+                    }
+                    for (int b = 64; b < n; b++) {
+                        const uint32_t kb = readlane(ka1, b - 64);
+                        const int ib = (int)readlane((uint32_t)ia1, b - 64);
+                        rk0 += (kb < ka0) || (kb == ka0 && ib < ia0);
+                        rk1 += (kb < ka1) || (kb == ka1 && ib < ia1);
+                    }
+                    if (lane < n) {
+                        sm.nl.ws[rk0] = sm.nl.w[lane];
+                        sm.nl.at[rk0] = (int16_t)lane;
+                    }
+                    if (lane + 64 < n) {
+                        sm.nl.ws[rk1] = sm.nl.w[lane + 64];
+                        sm.nl.at[rk1] = (int16_t)(lane + 64);
+                    }
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    const int r0 = 2 * lane;
+                    const double w0 = r0 < n ? sm.nl.ws[r0] : 0.0;
+                    const double w1 = r0 + 1 < n ? sm.nl.ws[r0 + 1] : 0.0;
+                    const double c0 = below + wave_incl_sum(w0 + w1) - (w0 + w1);  // before rank r0
+                    int prank = -1;
+                    if (r0 < n && T >= c0 && T - c0 < w0) prank = r0;
+                    else if (r0 + 1 < n && T >= c0 + w0 && T - (c0 + w0) < w1) prank = r0 + 1;
+                    const uint64_t bal = __ballot(prank >= 0);
+                    // the bucket holds the crossing, so exactly one rank qualifies
+                    const int pl = bal ? (int)__builtin_ctzll(bal) : 0;
+                    const double pbelow = readlane_d(prank == r0 ? c0 : c0 + w0, pl);
+                    prank = bal ? (int)readlane((uint32_t)prank, pl) : n - 1;
+                    // the crossing bucket's kept part (ranks >= prank) joins its sweeps' kept mass
+                    if (r0 < n && r0 >= prank) atomicAdd(&sm.ctl.kept[sm.nl.idx[sm.nl.at[r0]] / kSW], w0);
+                    if (r0 + 1 < n && r0 + 1 >= prank) atomicAdd(&sm.ctl.kept[sm.nl.idx[sm.nl.at[r0 + 1]] / kSW], w1);
+                    if (lane == 0) {
+                        const int at = sm.nl.at[prank];
+                        sm.ctl.sel_key = sm.nl.key[at];
+                        sm.ctl.sel_idx = sm.nl.idx[at];
+                        sm.ctl.sel_cbelow = pbelow;
+                    }
+                }
+                g.sync();
+                dc = key2f(sm.ctl.sel_key);
+                ic = sm.ctl.sel_idx;
+                cbelow = sm.ctl.sel_cbelow;
+#pragma unroll
+                for (int c = 0; c < NC; c++) kc[c] = sm.ctl.kept[c];
+            }
+        }
+        if (!fast) {
+            // no crossing (top_p at or below 0), or a crowded crossing bucket: the general select
+            // over the whole row, then the kept mass per sweep by a full pass
+            for (int b = g.t; b < kNB; b += kT) sm.u.sel.hist[b] = 0.0;
+            uint64_t act = 0;
+#pragma unroll
+            for (int e = 0; e < NE; e++)
+                if (v[e] != kNegInf) act |= 1ull << e;
+            const float sc2 = lo < -1e-30f ? (float)kNB / -lo : 0.0f;
+            const float of2 = -lo * sc2;
+            auto b1 = [&](int e) -> int {
+                float x = v[e];
+                asm volatile("" : "+v"(x));
+                return (int)__builtin_amdgcn_fmed3f(__builtin_fmaf(x, sc2, of2), 0.0f, (float)(kNB - 1));
+            };
+            g.sync();
+            uint32_t ck;
+            block_select<NC>(g, sm, act, T, true, keyof, qof, b1, kSiteScanP, kSiteLRankP, ck, ic, cbelow);
+            dc = key2f(ck);
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                double s2 = 0.0;
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (kept(c * 4 + j)) s2 += qof(c * 4 + j);
+                const double w = wave_sum(s2);
+                if (g.lane == 0) g.slot[kSiteChunk0 + c][g.wv] = (uint64_t)__double_as_longlong(w);
+            }
+            g.sync();
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                double s2 = 0.0;
+#pragma unroll
+                for (int w = 0; w < kWaves; w++) s2 += __longlong_as_double((long long)g.slot[kSiteChunk0 + c][w]);
+                kc[c] = s2;
+            }
+        }
+        Skept = S - cbelow;
+    } else {
+        // no top-p: every finite entry is kept; per-sweep totals from one pass
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            double s2 = 0.0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) s2 += fixed_point((double)exp_neg(v[c * 4 + j]), scaleF);
+            const double w = wave_sum(s2);
+            if (g.lane == 0) g.slot[kSiteChunk0 + c][g.wv] = (uint64_t)__double_as_longlong(w);
+        }
+        g.sync();
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            double s2 = 0.0;
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) s2 += __longlong_as_double((long long)g.slot[kSiteChunk0 + c][w]);
+            kc[c] = s2;
+            S += s2;
+        }
+        Skept = S;
     }
+
+    // ---- draw: first kept index (index order) whose inclusive prefix mass exceeds floor(u * Skept)
+    const double D = floor(u * Skept);
+    int cstar = -1;
+    double run = 0.0;
+#pragma unroll
+    for (int c = 0; c < NC; c++)
+        if (cstar < 0) {
+            if (D >= run && D - run < kc[c]) cstar = c;
+            else run += kc[c];
+        }
     int pick = -1;
     if (cstar >= 0) {
-        uint64_t mine = 0;
+        double w4[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) w4[j] = 0.0;
 #pragma unroll
         for (int c = 0; c < NC; c++)
-            if (c == cstar) mine = cs[c];
-        uint64_t total;
-        const uint64_t excl = block_excl_scan(mine, ctl.r64, total);
-        if (tid == 0) ctl.found_idx = -1;
-        __syncthreads();
+            if (c == cstar) {  // uniform: only the sweep holding the draw is revisited
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (kept(c * 4 + j)) w4[j] = qof(c * 4 + j);
+            }
+        const double mine = w4[0] + w4[1] + w4[2] + w4[3];
+        if (g.t == 0) sm.ctl.found = -1;
+        double total;
+        const double excl = g.excl_scan(mine, kSiteDraw, total);
         if (D >= run + excl && D - (run + excl) < mine) {
-            uint64_t acc = run + excl;
+            double acc = run + excl;
 #pragma unroll
-            for (int c = 0; c < NC; c++)
-                if (c == cstar)
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const int e = c * 4 + j;
-                        if ((kept >> e) & 1u) {
-                            acc += wgt[e];
-                            if (D < acc) {
-                                ctl.found_idx = elem_index(e);
-                                break;
-                            }
-                        }
-                    }
+            for (int j = 0; j < 4; j++) {
+                acc += w4[j];
+                if (w4[j] > 0.0 && D < acc) {
+                    sm.ctl.found = cstar * kSW + g.t * 4 + j;
+                    break;
+                }
+            }
         }
-        __syncthreads();
-        pick = ctl.found_idx;
+        g.sync();
+        pick = sm.ctl.found;
     }
-    if (pick < 0) {  // no crossing: the last kept id with p > 0
+    if (pick < 0) {  // no crossing: the last kept id with p > 0 (exp underflows below -745.133)
         int li = -1;
 #pragma unroll
         for (int e = 0; e < NE; e++)
-            if (((kept >> e) & 1u) && ((positive >> e) & 1u)) li = max(li, elem_index(e));
-        pick = block_imax(li, ctl.ri);
+            if (kept(e) && v[e] >= -745.1331787109375f) li = max(li, eidx(e));
+        pick = g.imax(li, kSiteLast);
         if (pick < 0) pick = 0;
     }
-    if (tid == 0) a.out_ids[r] = pick;
+    if (g.t == 0) a.out_ids[r] = pick;
     if (prow) {
         double se = 0.0;
 #pragma unroll
         for (int e = 0; e < NE; e++)
-            if ((kept >> e) & 1u) se += exp((double)(v[e] - m));
-        se = block_sum(se, ctl.rd);
+            if (kept(e)) se += (double)exp_neg(v[e]);
+        se = g.dsum(se, kSitePSum);
 #pragma unroll
         for (int e = 0; e < NE; e++)
-            if ((valid >> e) & 1u) prow[elem_index(e)] = ((kept >> e) & 1u) ? exp((double)(v[e] - m)) / se : 0.0;
+            if (eidx(e) < V) prow[eidx(e)] = kept(e) ? (double)exp_neg(v[e]) / se : 0.0;
     }
 }
 
 template <int NC>
-hipError_t launch_nc(const SampleArgs& a, bool vec, hipStream_t stream) {
-    const dim3 grid(a.rows), block(kThreads);
-    if (vec)
-        hipLaunchKernelGGL((sample_rows_kernel<NC, true>), grid, block, 0, stream, a);
-    else
-        hipLaunchKernelGGL((sample_rows_kernel<NC, false>), grid, block, 0, stream, a);
+hipError_t launch_nc(const SampleArgs& a, int vec, hipStream_t stream) {
+    hipLaunchKernelGGL((sample_rows_kernel<NC>), dim3(a.rows), dim3(kT), 0, stream, a, vec);
     return hipGetLastError();
 }
 
@@ -915,19 +1160,14 @@ hipError_t launch_nc(const SampleArgs& a, bool vec, hipStream_t stream) {
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream) {
     if (a.rows <= 0) return hipSuccess;
     if (a.vocab <= 0 || a.vocab > kRowResidentMaxVocab) return hipErrorNotSupported;
-    const int nc = (a.vocab + kSweep - 1) / kSweep;
-    const bool vec = (a.vocab % 4 == 0) && (a.ld % 4 == 0) && (((uintptr_t)a.logits & 15u) == 0);
-    switch (nc) {
-        case 1: return launch_nc<1>(a, vec, stream);
-        case 2: return launch_nc<2>(a, vec, stream);
-        case 3: return launch_nc<3>(a, vec, stream);
-        case 4: return launch_nc<4>(a, vec, stream);
-        case 5: return launch_nc<5>(a, vec, stream);
-        case 6: return launch_nc<6>(a, vec, stream);
-        case 7: return launch_nc<7>(a, vec, stream);
-        case 8: return launch_nc<8>(a, vec, stream);
-        default: return hipErrorNotSupported;
-    }
+    const int vec = (a.ld % 4 == 0) && (((uintptr_t)a.logits & 15u) == 0) ? 1 : 0;
+    const int V = a.vocab;
+    if (V <= 1024) return launch_nc<1>(a, vec, stream);
+    if (V <= 2048) return launch_nc<2>(a, vec, stream);
+    if (V <= 3072) return launch_nc<3>(a, vec, stream);
+    if (V <= 4096) return launch_nc<4>(a, vec, stream);
+    if (V <= 6144) return launch_nc<6>(a, vec, stream);
+    return launch_nc<8>(a, vec, stream);
 }
 
 }  // namespace vxs
