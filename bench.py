@@ -77,6 +77,37 @@ def summarize_trace(path: str) -> None:
               f"{d[-1] / 1e3:9.3f}  {grid}  {wg}  {name[:110]}")
 
 
+def _read_pmc(path: str):
+    import csv
+    from collections import defaultdict
+
+    acc = defaultdict(lambda: defaultdict(list))
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            name = row.get("Kernel_Name") or row.get("KernelName") or "?"
+            counter = row.get("Counter_Name") or row.get("Counter")
+            acc[name][counter].append(float(row.get("Counter_Value") or row.get("Value")))
+    return acc
+
+
+def summarize_pmc(path: str, copy_path: str, copy_mib: int) -> None:
+    """Average counters per kernel. FETCH_SIZE/WRITE_SIZE (KiB per dispatch) are scaled by the factor
+    that maps the same counter over a device-to-device copy of copy_mib MiB (which reads and writes
+    copy_mib MiB) to its true size."""
+    factor = {}
+    for name, counters in _read_pmc(copy_path).items():
+        for c, vals in counters.items():
+            avg = sum(vals) / len(vals)
+            factor[c] = copy_mib * 1024.0 / avg
+            print(f"calibration {c}: {avg:.0f} KiB per dispatch for a {copy_mib} MiB copy -> factor "
+                  f"{factor[c]:.4f} ({len(vals)} dispatches of {name[:60]})")
+    for name, counters in _read_pmc(path).items():
+        for c, vals in counters.items():
+            avg = sum(vals) / len(vals)
+            print(f"{c}: {avg:.1f} KiB per dispatch raw, {avg * factor.get(c, 1.0) * 1024.0:.0f} bytes "
+                  f"calibrated ({len(vals)} dispatches)  {name[:90]}")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -86,10 +117,18 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=5, help="passes of the CPU oracle over the batch")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--summarize-trace", metavar="CSV")
+    ap.add_argument("--summarize-pmc", nargs=3, metavar=("COUNTER_CSV", "COPY_CSV", "COPY_MIB"),
+                    help="per-kernel average of a rocprofv3 --pmc counter_collection.csv, calibrated by the "
+                         "same counter over the copies of COPY_MIB MiB that --calibrate-copy makes")
+    ap.add_argument("--calibrate-copy", type=int, metavar="MIB",
+                    help="only run 5 device-to-device copies of MIB MiB (the counter calibration workload)")
     args = ap.parse_args()
 
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
+        return 0
+    if args.summarize_pmc:
+        summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], int(args.summarize_pmc[2]))
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (the sampler's rows are "
@@ -100,6 +139,15 @@ def main() -> int:
 
     from voxwerk_amd import hip, workloads
     from voxwerk_amd.sampler import Context
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy << 20
+        src, dst = hip.DeviceArray((n,), np.uint8), hip.DeviceArray((n,), np.uint8)
+        for _ in range(5):
+            dst.copy_from(src)
+        hip.synchronize()
+        log(f"[bench] 5 device-to-device copies of {args.calibrate_copy} MiB done")
+        return 0
 
     w = workloads.workload(4)
     rows, vocab = w.rows, w.vocab
@@ -158,14 +206,16 @@ def main() -> int:
     w1 = workloads.workload(1)
     b1 = w1.generate()
     lat = []
-    for i in range(200 + args.latency_steps):
+    for i in range(200 + args.latency_steps if args.latency_steps > 0 else 0):
         t = time.perf_counter_ns()
         ctx.sample(b1.logits, b1.params, b1.u, b1.hist_off, b1.hist_ids)
         if i >= 200:
             lat.append(time.perf_counter_ns() - t)
-    lat = np.sort(np.array(lat)) / 1e3
-    p50, p99 = float(lat[len(lat) // 2]), float(lat[int(len(lat) * 0.99)])
-    log(f"[bench] talker step 1x3072 host-to-host: p50 {p50:.1f} us, p99 {p99:.1f} us")
+    p50 = p99 = None
+    if lat:
+        lat = np.sort(np.array(lat)) / 1e3
+        p50, p99 = round(float(lat[len(lat) // 2]), 2), round(float(lat[int(len(lat) * 0.99)]), 2)
+        log(f"[bench] talker step 1x3072 host-to-host: p50 {p50:.1f} us, p99 {p99:.1f} us")
 
     cpu = None
     parity = None
@@ -220,7 +270,7 @@ def main() -> int:
         },
         "hbm_gbps": round(gbps, 1),
         "hbm_pct_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
-        "latency_1row_us": {"p50": round(p50, 2), "p99": round(p99, 2), "workload": "talker_step 1x3072 host-to-host"},
+        "latency_1row_us": {"p50": p50, "p99": p99, "workload": "talker_step 1x3072 host-to-host"},
         "roofline": {
             "bound": "hbm",
             "achieved": round(gbps, 1),
