@@ -41,6 +41,8 @@ def select(x: np.ndarray, do_sample, top_k, top_p, temperature, u):
     """Sampler.cs:35-88 on a float32 row (modified in place). Returns (id, probs or None)."""
     n = x.size
     if not do_sample:
+        if np.isnan(x).any():
+            raise ValueError("NaN logits")
         return int(np.argmax(x)), None
     inv = F32(1.0) / F32(temperature)
     x *= inv

@@ -116,6 +116,8 @@ static int sample_row(int n, float* x, const int32_t* hist, int64_t nhist, const
     suppress_row(n, x, p);
 
     if (!p->do_sample) { /* Sampler.cs:37 — greedy, no temperature, no draw */
+        for (int i = 0; i < n; i++) /* the ABI rejects NaN (outside the C# contract) */
+            if (isnan(x[i])) return VXS_ERR_NONFINITE;
         *out_id = vxs_oracle_argmax(n, x);
         return VXS_OK;
     }
