@@ -114,7 +114,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=5000)
     ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--latency-steps", type=int, default=10000)
-    ap.add_argument("--cpu-reps", type=int, default=5, help="passes of the CPU oracle over the batch")
+    ap.add_argument("--cpu-reps", type=int, default=15, help="passes of the CPU oracle over the batch")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--summarize-trace", metavar="CSV")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("COUNTER_CSV", "COPY_CSV", "COPY_MIB"),
