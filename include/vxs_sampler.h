@@ -41,6 +41,10 @@ extern "C" {
 
 /* flags for vxs_sample / vxs_sample_device */
 #define VXS_FLAG_NONE 0u
+/* Kernel selection; without either flag the library chooses (one wave per row for batches of at
+ * least 1024 rows with vocab <= 3072, else one workgroup per row). Results are identical. */
+#define VXS_FLAG_PATH_BLOCK (1u << 8) /* one 256-thread workgroup per row                      */
+#define VXS_FLAG_PATH_WAVE (1u << 9)  /* one wave per row first, 4 rows per workgroup (vocab <= 3072) */
 
 /*
  * Per-row sampling parameters (blittable; 36 bytes, 4-byte aligned).

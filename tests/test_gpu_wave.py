@@ -1,0 +1,106 @@
+"""GPU parity of the one-wave-per-row path (VXS_FLAG_PATH_WAVE): ids against the CPU oracle and
+identical to the one-workgroup-per-row path on the same rows, over the workloads, option mixes and the
+rows the wave path hands back to the general algorithm (top-k, few candidates, crowded or degenerate
+top-p cuts, requested outputs)."""
+import numpy as np
+import pytest
+
+from oracle import ref
+from parity import compare_ids
+from voxwerk_amd import workloads
+from voxwerk_amd._lib import PARAMS_DTYPE
+
+pytestmark = pytest.mark.gpu
+
+
+def run_both_paths(ctx, logits, params, u=None, off=None, hist=None, label=""):
+    wave = ctx.sample(logits, params, u, off, hist, path="wave", raise_on_error=False)
+    block = ctx.sample(logits, params, u, off, hist, path="block", raise_on_error=False)
+    ora = ref.sample(logits, params, u, off, hist, threads=8)
+    rep = compare_ids(wave, ora)
+    print(f"{label}: wave {rep}", flush=True)
+    assert not rep.unexplained, f"{label}: wave path ids differ at rows {rep.unexplained[:10]}"
+    assert np.array_equal(wave, block), f"{label}: wave and block paths disagree"
+    return wave, ora
+
+
+@pytest.mark.parametrize("wid", [1, 3, 4])
+def test_wave_workloads(ctx, wid):
+    w = workloads.workload(wid)
+    b = w.generate()
+    run_both_paths(ctx, b.logits, b.params, b.u, b.hist_off, b.hist_ids, label=w.name)
+
+
+def test_wave_code_predictor(ctx):
+    w = workloads.workload(2)
+    for step in range(0, w.steps, 4):
+        b = w.generate(step=step)
+        run_both_paths(ctx, b.logits, b.params, b.u, b.hist_off, b.hist_ids, label=f"{w.name}[{step}]")
+
+
+@pytest.mark.parametrize("vocab", [7, 64, 300, 1000, 2048, 2500, 3001, 3072])
+def test_wave_option_mixes(ctx, vocab):
+    """Mostly full-vocabulary rows (the wave path's own work), some top-k and greedy rows."""
+    rng = np.random.default_rng(2000 + vocab)
+    rows = 256
+    scale = rng.choice([0.3, 1.0, 3.0, 8.0], size=(rows, 1))
+    logits = (rng.standard_normal((rows, vocab)) * scale).astype(np.float32)
+    logits[rng.random((rows, vocab)) < 0.02] += 5.0
+    hl = rng.integers(0, 700, size=rows)
+    off = np.zeros(rows + 1, np.int32)
+    off[1:] = np.cumsum(hl)
+    hist = rng.integers(0, vocab, size=off[-1]).astype(np.int32)
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = (rng.random(rows) > 0.1).astype(np.int32)
+    p["top_k"] = np.where(rng.random(rows) < 0.15, rng.integers(1, 300, rows), 0)
+    p["top_p"] = rng.choice([1.0, 0.99, 0.95, 0.9, 0.8, 0.5, 0.2, 1e-6], size=rows).astype(np.float32)
+    p["temperature"] = rng.choice([0.5, 0.7, 0.9, 1.0, 1.3], size=rows).astype(np.float32)
+    p["rep_penalty"] = rng.choice([1.0, 1.05, 1.1, 0.9], size=rows).astype(np.float32)
+    supp = rng.random(rows) < 0.3
+    p["supp_begin"] = np.where(supp, vocab // 3, 0)
+    p["supp_end"] = np.where(supp, vocab, 0)
+    p["keep_id"] = np.where(supp, vocab // 2, -1)
+    p["ban_id"] = np.where(rng.random(rows) < 0.1, vocab // 2, -1)
+    run_both_paths(ctx, logits, p, rng.random(rows), off, hist, label=f"mixed V={vocab}")
+
+
+def test_wave_deferred_and_special_rows(ctx):
+    vocab = 3072
+    rng = np.random.default_rng(31)
+    rows = 12
+    x = (rng.standard_normal((rows, vocab)) * 2).astype(np.float32)
+    x[0] = 0.25                 # uniform row: one crowded crossing bucket
+    x[1, :] = -np.inf           # all masked
+    x[1, 5] = 1.0
+    x[2, 7] = np.nan            # rejected
+    x[3, 9] = np.inf            # rejected
+    x[4, :3000] = -np.inf       # 72 candidates: exact regime
+    x[5] = np.round(x[5])       # many exact ties
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = 1
+    p["top_p"] = [0.5, 0.9, 0.9, 0.9, 0.9, 0.7, 1e-7, 0.0, 1.0, 0.95, 0.95, 0.95]
+    p["temperature"] = [1.0] * 9 + [-1.0, 1e-3, 1e3]
+    p["rep_penalty"] = 1.0
+    p["keep_id"] = -1
+    p["ban_id"] = -1
+    u = np.linspace(0.02, 0.98, rows)
+    wave, ora = run_both_paths(ctx, x, p, u, label="special rows")
+    assert wave[2] == -3 and wave[3] == -3
+
+
+def test_wave_history_errors(ctx):
+    x = np.zeros((1024, 2048), np.float32)
+    p = np.zeros(1024, dtype=PARAMS_DTYPE)
+    p["do_sample"] = 1
+    p["top_p"] = 0.9
+    p["temperature"] = 1.0
+    p["rep_penalty"] = 1.1
+    p["keep_id"] = -1
+    p["ban_id"] = -1
+    off = (np.arange(1025) * 2).astype(np.int32)
+    hist = np.tile(np.array([1, 2], np.int32), 1024)
+    hist[7] = 2048
+    hist[100] = -5
+    ids = ctx.sample(x, p, np.full(1024, 0.5), off, hist, path="wave", raise_on_error=False)
+    assert ids[3] == -2 and ids[50] == -2
+    assert (np.delete(ids, [3, 50]) >= 0).all()

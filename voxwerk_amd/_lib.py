@@ -26,6 +26,8 @@ VXS_ERR_NONFINITE = -3
 VXS_ERR_HIP = -4
 VXS_ERR_UNSUPPORTED = -5
 VXS_ERR_NO_DEVICE = -6
+VXS_FLAG_PATH_BLOCK = 1 << 8
+VXS_FLAG_PATH_WAVE = 1 << 9
 
 
 class VxsParams(ctypes.Structure):

@@ -73,6 +73,9 @@ struct vxs_ctx {
     hipStream_t stream = nullptr;
     std::string err;
     DevBuf d_in, d_ids, d_logits_out, d_probs_out;
+    DevBuf d_defer;  // deferral list of the one-wave path: 2 counters, then one entry per row
+    size_t defer_rows = 0;
+    int defer_phase = 0;  // which counter the next call uses
     HostBuf h_in, h_ids, h_out;
 };
 
@@ -178,10 +181,50 @@ int check_hist_host(vxs_ctx* ctx, int rows, const int32_t* hist_off, const int32
     return VXS_OK;
 }
 
+constexpr uint32_t kPathFlags = VXS_FLAG_PATH_BLOCK | VXS_FLAG_PATH_WAVE;
+
+// Kernel path: the one-wave path needs a vocabulary it can hold and enough rows to fill the GPU
+// at four rows per workgroup; the caller may force either.
+int choose_path(uint32_t flags, int rows, int vocab) {
+    if (vocab > vxs::kWaveMaxVocab || (flags & VXS_FLAG_PATH_BLOCK)) return vxs::kPathBlock;
+    if (flags & VXS_FLAG_PATH_WAVE) return vxs::kPathQuad;
+    return rows >= 1024 ? vxs::kPathQuad : vxs::kPathBlock;
+}
+
+// Deferral list for `rows` rows. Both counters are zeroed when the buffer is (re)allocated; after
+// that each call's deferral kernel zeroes the counter of the call after it.
+hipError_t ensure_defer(vxs_ctx* ctx, int rows, vxs::SampleArgs& a) {
+    if ((size_t)rows > ctx->defer_rows) {
+        hipError_t e = ctx->d_defer.reserve(sizeof(int32_t) * (2 + (size_t)rows));
+        if (e != hipSuccess) return e;
+        if ((e = hipMemset(ctx->d_defer.p, 0, 2 * sizeof(int32_t))) != hipSuccess) return e;
+        ctx->defer_rows = ctx->d_defer.cap / sizeof(int32_t) - 2;
+    }
+    int32_t* counts = static_cast<int32_t*>(ctx->d_defer.p);
+    a.defer_count = counts + ctx->defer_phase;
+    a.defer_next = counts + (ctx->defer_phase ^ 1);
+    a.defer_list = counts + 2;
+    ctx->defer_phase ^= 1;
+    return hipSuccess;
+}
+
+// A failed launch may leave a deferral counter unreset: zero both again before the next use.
+hipError_t launch_checked(vxs_ctx* ctx, const vxs::SampleArgs& a) {
+    const hipError_t e = vxs::launch_sample(a, ctx->stream);
+    if (e != hipSuccess) ctx->defer_rows = 0;
+    return e;
+}
+
+int check_flags(vxs_ctx* ctx, uint32_t flags) {
+    if (flags & ~kPathFlags) return fail(ctx, VXS_ERR_INVALID_ARG, "unknown flags");
+    if ((flags & kPathFlags) == kPathFlags) return fail(ctx, VXS_ERR_INVALID_ARG, "both path flags set");
+    return VXS_OK;
+}
+
 // Stage inputs and launch. On success the kernel is queued on ctx->stream.
 int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int64_t ld, const int32_t* hist_off,
                      const int32_t* hist_ids, const vxs_params* params, int params_stride, const double* u,
-                     bool want_logits, bool want_probs, uint32_t kflags) {
+                     bool want_logits, bool want_probs, uint32_t kflags, uint32_t flags = 0) {
     const Layout L = plan(rows, vocab, params_stride, hist_off);
     VXS_HIP(ctx, ctx->h_in.reserve(L.total));
     VXS_HIP(ctx, ctx->d_in.reserve(L.total));
@@ -221,7 +264,9 @@ int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int
     a.out_logits = want_logits ? static_cast<float*>(ctx->d_logits_out.p) : nullptr;
     a.out_probs = want_probs ? static_cast<double*>(ctx->d_probs_out.p) : nullptr;
     a.kflags = kflags;
-    VXS_HIP(ctx, vxs::launch_sample(a, ctx->stream));
+    a.path = choose_path(flags, rows, vocab);
+    if (a.path == vxs::kPathQuad) VXS_HIP(ctx, ensure_defer(ctx, rows, a));
+    VXS_HIP(ctx, launch_checked(ctx, a));
     return VXS_OK;
 }
 
@@ -281,6 +326,7 @@ VXS_API void vxs_destroy(vxs_ctx* ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     ctx->d_in.release();
     ctx->d_ids.release();
+    ctx->d_defer.release();
     ctx->d_logits_out.release();
     ctx->d_probs_out.release();
     ctx->h_in.release();
@@ -313,13 +359,13 @@ VXS_API int vxs_sample(vxs_ctx* ctx, int rows, int vocab, const float* logits, i
     try {
         int rc = check_shape(ctx, rows, vocab, logits, ld, params, params_stride, out_ids);
         if (rc != VXS_OK) return rc;
-        if (flags != VXS_FLAG_NONE) return fail(ctx, VXS_ERR_INVALID_ARG, "unknown flags");
+        if ((rc = check_flags(ctx, flags)) != VXS_OK) return rc;
         if (rows == 0) return VXS_OK;
         if ((rc = check_params_host(ctx, rows, params, params_stride, u)) != VXS_OK) return rc;
         if ((rc = check_hist_host(ctx, rows, hist_off, hist_ids)) != VXS_OK) return rc;
         VXS_HIP(ctx, hipSetDevice(ctx->device));
         rc = stage_and_launch(ctx, rows, vocab, logits, ld, hist_off, hist_ids, params, params_stride, u,
-                              out_logits != nullptr, out_probs != nullptr, 0);
+                              out_logits != nullptr, out_probs != nullptr, 0, flags);
         if (rc != VXS_OK) return rc;
         if ((rc = fetch(ctx, out_ids, ctx->d_ids.p, sizeof(int32_t) * (size_t)rows)) != VXS_OK) return rc;
         if (out_logits && (rc = fetch(ctx, out_logits, ctx->d_logits_out.p, sizeof(float) * (size_t)rows * vocab)) != VXS_OK)
@@ -342,7 +388,7 @@ VXS_API int vxs_sample_device(vxs_ctx* ctx, int rows, int vocab, const float* d_
     try {
         int rc = check_shape(ctx, rows, vocab, d_logits, ld, d_params, params_stride, d_out_ids);
         if (rc != VXS_OK) return rc;
-        if (flags != VXS_FLAG_NONE) return fail(ctx, VXS_ERR_INVALID_ARG, "unknown flags");
+        if ((rc = check_flags(ctx, flags)) != VXS_OK) return rc;
         if (rows == 0) return VXS_OK;
         if (d_hist_off && !d_hist_ids) return fail(ctx, VXS_ERR_INVALID_ARG, "hist_ids is NULL");
         if (params_stride > 1) return fail(ctx, VXS_ERR_INVALID_ARG, "device params_stride must be 0 or 1");
@@ -361,7 +407,9 @@ VXS_API int vxs_sample_device(vxs_ctx* ctx, int rows, int vocab, const float* d_
         a.out_logits = d_out_logits;
         a.out_probs = d_out_probs;
         a.kflags = 0;
-        VXS_HIP(ctx, vxs::launch_sample(a, ctx->stream));
+        a.path = choose_path(flags, rows, vocab);
+        if (a.path == vxs::kPathQuad) VXS_HIP(ctx, ensure_defer(ctx, rows, a));
+        VXS_HIP(ctx, launch_checked(ctx, a));
         ctx->err.clear();
         return VXS_OK;
     } catch (...) {

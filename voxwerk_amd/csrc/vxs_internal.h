@@ -27,10 +27,24 @@ struct SampleArgs {
     float* out_logits;   // optional [rows][vocab]
     double* out_probs;   // optional [rows][vocab]
     uint32_t kflags;
+    int path;            // kPathBlock or kPathQuad
+    // kPathQuad: rows the one-wave path hands back, appended by it and sampled by a second
+    // kernel. Calls alternate between two counters: this call appends at *defer_count, and its
+    // second kernel zeroes *defer_next, the counter of the following call.
+    int32_t* defer_list;  // [rows]
+    int32_t* defer_count;
+    int32_t* defer_next;
 };
 
-// Largest vocabulary handled by the row-resident kernel (one workgroup keeps a row in VGPRs).
+enum : int {
+    kPathBlock = 0,  // one 256-thread workgroup per row
+    kPathQuad = 1,   // one wave per row first, four rows per workgroup (vocab <= kWaveMaxVocab)
+};
+
+// Largest vocabulary handled by the row-resident kernels (a row stays in VGPRs).
 constexpr int kRowResidentMaxVocab = 8192;
+// Largest vocabulary of the one-wave-per-row fast path (vxs_wave.h).
+constexpr int kWaveMaxVocab = 3072;
 
 // Enqueue the sampler on `stream`. Returns hipSuccess or the launch error.
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream);

@@ -30,6 +30,7 @@
 
 #include "vxs_device.h"
 #include "vxs_internal.h"
+#include "vxs_wave.h"
 
 namespace vxs {
 namespace {
@@ -478,19 +479,17 @@ __device__ __forceinline__ void block_select(const Blk& g, RowSmem<NC>& sm, uint
 template <int NC>
 constexpr int kWavesPerEu = NC <= 3 ? 4 : 1;
 
+// One row by the whole 256-thread workgroup (every thread calls it; it returns uniformly).
 template <int NC>
-__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<NC>))) void sample_rows_kernel(
-    SampleArgs a, int vec) {
+__device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, RowSmem<NC>& sm) {
     using C = Cfg<NC>;
     constexpr int NE = C::NE;
-    __shared__ RowSmem<NC> sm;
 
     Blk g;
     g.lane = threadIdx.x & 63;
     g.wv = threadIdx.x >> 6;
     g.t = threadIdx.x;
     g.slot = sm.slot;
-    const int r = blockIdx.x;
     auto eidx = [&](int e) { return (e >> 2) * kSW + g.t * 4 + (e & 3); };
 
     const int V = a.vocab;
@@ -1150,8 +1149,57 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<
 }
 
 template <int NC>
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<NC>))) void sample_rows_kernel(
+    SampleArgs a, int vec) {
+    __shared__ RowSmem<NC> sm;
+    row_block<NC>(a, vec, blockIdx.x, sm);
+}
+
+// Four rows per workgroup, one per wave, through the one-wave fast path (vxs_wave.h). A row the
+// fast path hands back is appended to the deferral list for sample_deferred_kernel.
+template <int NS>
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void sample_quad_kernel(SampleArgs a,
+                                                                                                int vec) {
+    __shared__ WaveSmem<NS> sm[kWaves];
+    const int wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * kWaves + wv;
+    if (r >= a.rows) return;
+    if (wave_fast_row<NS>(a, vec, r, lane, sm[wv]) && lane == 0) a.defer_list[atomicAdd(a.defer_count, 1)] = r;
+}
+
+// The deferred rows, one per workgroup with the general algorithm; a grid-stride loop over the
+// list, which is usually empty. Block 0 zeroes the next call's counter (nothing else uses it now).
+template <int NC>
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(2))) void sample_deferred_kernel(SampleArgs a,
+                                                                                                    int vec) {
+    __shared__ RowSmem<NC> sm;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *a.defer_next = 0;
+    const int n = __hip_atomic_load(a.defer_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll 1
+    for (int i = blockIdx.x; i < n; i += gridDim.x) {
+        const int r = __builtin_amdgcn_readfirstlane(a.defer_list[i]);
+        row_block<NC>(a, vec, r, sm);
+        __syncthreads();
+    }
+}
+
+template <int NC>
 hipError_t launch_nc(const SampleArgs& a, int vec, hipStream_t stream) {
     hipLaunchKernelGGL((sample_rows_kernel<NC>), dim3(a.rows), dim3(kT), 0, stream, a, vec);
+    return hipGetLastError();
+}
+
+// Blocks of the deferral kernel: enough to sample a long list quickly, few enough that an empty
+// list costs little.
+constexpr int kDeferBlocks = 256;
+
+template <int NS, int NC>
+hipError_t launch_quad(const SampleArgs& a, int vec, hipStream_t stream) {
+    hipLaunchKernelGGL((sample_quad_kernel<NS>), dim3((a.rows + kWaves - 1) / kWaves), dim3(kT), 0, stream, a, vec);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((sample_deferred_kernel<NC>), dim3(kDeferBlocks), dim3(kT), 0, stream, a, vec);
     return hipGetLastError();
 }
 
@@ -1162,6 +1210,11 @@ hipError_t launch_sample(const SampleArgs& a, hipStream_t stream) {
     if (a.vocab <= 0 || a.vocab > kRowResidentMaxVocab) return hipErrorNotSupported;
     const int vec = (a.ld % 4 == 0) && (((uintptr_t)a.logits & 15u) == 0) ? 1 : 0;
     const int V = a.vocab;
+    if (a.path == kPathQuad && V <= kWaveMaxVocab) {
+        if (V <= 1024) return launch_quad<4, 1>(a, vec, stream);
+        if (V <= 2048) return launch_quad<8, 2>(a, vec, stream);
+        return launch_quad<12, 3>(a, vec, stream);
+    }
     if (V <= 1024) return launch_nc<1>(a, vec, stream);
     if (V <= 2048) return launch_nc<2>(a, vec, stream);
     if (V <= 3072) return launch_nc<3>(a, vec, stream);

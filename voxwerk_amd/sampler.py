@@ -189,8 +189,14 @@ def _csr(histories: Optional[Iterable[Iterable[int]]], rows: int):
     return off.astype(np.int32), np.ascontiguousarray(ids, dtype=np.int32)
 
 
+PATH_FLAGS = {"auto": 0, "block": _lib.VXS_FLAG_PATH_BLOCK, "wave": _lib.VXS_FLAG_PATH_WAVE}
+
+
 class Context:
-    """Owns one vxs_ctx (one HIP stream). Not thread-safe; use one per thread."""
+    """Owns one vxs_ctx (one HIP stream). Not thread-safe; use one per thread.
+
+    ``path`` of the sampling calls selects the kernel: "auto" (the library chooses), "block" (one
+    workgroup per row) or "wave" (one wave per row first, vocab <= 3072); results are identical."""
 
     def __init__(self, device: int = 0, max_rows: int = 0, max_vocab: int = 0, max_hist: int = 0):
         self._lib = load_vxs()
@@ -240,7 +246,8 @@ class Context:
     # host-memory batched call ----------------------------------------------------------------
     def sample(self, logits: np.ndarray, params: np.ndarray, u: Optional[np.ndarray] = None,
                hist_off: Optional[np.ndarray] = None, hist_ids: Optional[np.ndarray] = None,
-               want_logits: bool = False, want_probs: bool = False, raise_on_error: bool = True):
+               want_logits: bool = False, want_probs: bool = False, raise_on_error: bool = True,
+               path: str = "auto"):
         """Sample every row of `logits` [rows, vocab] (host). `params`: one PARAMS_DTYPE record
         (broadcast) or one per row. Returns ids (and the write-back logits / probabilities)."""
         logits = np.ascontiguousarray(logits, dtype=np.float32)
@@ -262,7 +269,8 @@ class Context:
         out_logits = np.empty((rows, vocab), dtype=np.float32) if want_logits else None
         out_probs = np.empty((rows, vocab), dtype=np.float64) if want_probs else None
         rc = self._lib.vxs_sample(self._h, rows, vocab, ptr(logits), vocab, ptr(hist_off), ptr(hist_ids),
-                                  ptr(params), stride, ptr(u), ptr(ids), ptr(out_logits), ptr(out_probs), 0)
+                                  ptr(params), stride, ptr(u), ptr(ids), ptr(out_logits), ptr(out_probs),
+                                  PATH_FLAGS[path])
         if rc != 0 and (raise_on_error or rc not in (_lib.VXS_ERR_ID_OUT_OF_RANGE, _lib.VXS_ERR_NONFINITE)):
             _raise(rc, self.last_error())
         if want_logits or want_probs:
@@ -271,10 +279,10 @@ class Context:
 
     # device-resident call (torch tensors or raw pointers) -----------------------------------------
     def sample_device(self, rows: int, vocab: int, logits, ld: int, params, params_stride: int, u, out_ids,
-                      hist_off=None, hist_ids=None, out_logits=None, out_probs=None) -> None:
+                      hist_off=None, hist_ids=None, out_logits=None, out_probs=None, path: str = "auto") -> None:
         rc = self._lib.vxs_sample_device(self._h, rows, vocab, ptr(logits), ld, ptr(hist_off), ptr(hist_ids),
                                          ptr(params), params_stride, ptr(u), ptr(out_ids), ptr(out_logits),
-                                         ptr(out_probs), 0)
+                                         ptr(out_probs), PATH_FLAGS[path])
         self._check(rc)
 
     def apply_repetition_penalty(self, logits: np.ndarray, hist_off: np.ndarray, hist_ids: np.ndarray,
