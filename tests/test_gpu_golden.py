@@ -42,7 +42,7 @@ def test_gpu_known_answers(ctx, case):
         assert np.array_equal(lg[0].view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("wid", [1, 2, 3, 4])
+@pytest.mark.parametrize("wid", [1, 2, 3, 4, 5])
 def test_gpu_matches_stored_ids(ctx, wid):
     m = META[str(wid)]
     w = workloads.workload(wid)

@@ -1,0 +1,106 @@
+"""GPU parity of the streaming kernel for vocabularies above 8192: the wide workload (1024 rows x
+151936, top-k 200, top-p 0.8, temperature 0.7, penalty over 4096 ids, suppression) and option mixes
+that take its general multi-pass path (top-k off or above 256, ties, greedy, degenerate rows),
+with write-back logits and probabilities against the CPU oracle."""
+import numpy as np
+import pytest
+
+from oracle import ref
+from parity import PROB_RTOL, comparable_rows, compare_ids, prob_rel_error
+from voxwerk_amd import workloads
+from voxwerk_amd._lib import PARAMS_DTYPE
+
+pytestmark = pytest.mark.gpu
+U32 = np.uint32
+
+
+def check_rows(ctx, logits, params, u=None, off=None, hist=None, label="", outputs=True):
+    if outputs:
+        ids, lg, pr = ctx.sample(logits, params, u, off, hist, want_logits=True, want_probs=True, raise_on_error=False)
+    else:
+        ids = ctx.sample(logits, params, u, off, hist, raise_on_error=False)
+    ora = ref.sample(logits, params, u, off, hist, threads=8, want_logits=outputs, want_probs=outputs)
+    rep = compare_ids(ids, ora)
+    print(f"{label}: {rep}", flush=True)
+    assert not rep.unexplained, f"{label}: ids differ at rows {rep.unexplained[:10]}"
+    if outputs:
+        ok = ids >= 0
+        assert np.array_equal(lg[ok].view(U32), ora["logits"][ok].view(U32)), f"{label}: write-back logits differ"
+        rel = prob_rel_error(pr, ora["probs"], comparable_rows(ids, ora) & ok)
+        assert rel <= PROB_RTOL, f"{label}: probability relative error {rel:.3e}"
+    return ids, ora
+
+
+def test_wide_workload(ctx):
+    w = workloads.workload(5)
+    b = w.generate(rows=256)
+    print(f"{w.name} rows={b.rows} vocab={w.vocab} digest={b.digest()[:16]}", flush=True)
+    check_rows(ctx, b.logits, b.params, b.u, b.hist_off, b.hist_ids, label=w.name, outputs=False)
+
+
+def test_wide_workload_outputs(ctx):
+    w = workloads.workload(5)
+    b = w.generate(rows=16)
+    check_rows(ctx, b.logits, b.params, b.u, b.hist_off, b.hist_ids, label=w.name + " outputs")
+
+
+@pytest.mark.parametrize("vocab", [8193, 20000, 151936])
+def test_wide_option_mixes(ctx, vocab):
+    rng = np.random.default_rng(3000 + vocab)
+    rows = 24
+    logits = (rng.standard_normal((rows, vocab)) * rng.choice([0.5, 2.0, 4.0], size=(rows, 1))).astype(np.float32)
+    logits[:, :50] += 4.0
+    logits[3] = np.round(logits[3])  # many ties
+    hl = rng.integers(0, 600, size=rows)
+    off = np.zeros(rows + 1, np.int32)
+    off[1:] = np.cumsum(hl)
+    hist = rng.integers(0, vocab, size=off[-1]).astype(np.int32)
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = 1
+    p["do_sample"][::6] = 0
+    p["top_k"] = rng.choice([0, 1, 50, 200, 256, 257, 1000], size=rows)
+    p["top_p"] = rng.choice([1.0, 0.95, 0.8, 0.3, 1e-6], size=rows).astype(np.float32)
+    p["temperature"] = rng.choice([0.7, 1.0, 1.3], size=rows).astype(np.float32)
+    p["rep_penalty"] = rng.choice([1.0, 1.05, 1.1], size=rows).astype(np.float32)
+    supp = rng.random(rows) < 0.4
+    p["supp_begin"] = np.where(supp, vocab - 1024, 0)
+    p["supp_end"] = np.where(supp, vocab, 0)
+    p["keep_id"] = np.where(supp, vocab - 1024 + 102, -1)
+    p["ban_id"] = -1
+    check_rows(ctx, logits, p, rng.random(rows), off, hist, label=f"wide mixed V={vocab}")
+
+
+def test_wide_special_rows(ctx):
+    vocab = 40000
+    rows = 8
+    x = np.full((rows, vocab), -1.0, np.float32)
+    x[0] = -np.inf                    # all masked: V-1
+    x[1] = 0.5                        # uniform: top-k ties, top-p by index order
+    x[2, 123] = np.nan                # rejected
+    x[3, 7] = 3.0
+    x[3, 39999] = 3.0                 # tied maxima
+    x[4] = np.linspace(-5, 5, vocab).astype(np.float32)
+    x[5, ::2] = -np.inf
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = [1, 1, 1, 1, 1, 1, 0, 1]
+    p["top_k"] = [50, 100, 0, 0, 0, 300, 0, 1]
+    p["top_p"] = [1.0, 0.5, 1.0, 1e-7, 0.9, 0.9, 1.0, 1.0]
+    p["temperature"] = 1.0
+    p["rep_penalty"] = 1.0
+    p["keep_id"] = -1
+    p["ban_id"] = -1
+    ids, ora = check_rows(ctx, x, p, np.linspace(0.05, 0.95, rows), label="wide special")
+    assert ids[0] == vocab - 1 and ids[2] == -3 and ids[3] == 39999
+
+
+def test_wide_penalty_only(ctx):
+    rng = np.random.default_rng(77)
+    vocab = 151936
+    x = rng.standard_normal((4, vocab)).astype(np.float32)
+    off = np.array([0, 100, 4196, 4196, 5000], np.int32)
+    hist = rng.integers(0, vocab, size=5000).astype(np.int32)
+    y = x.copy()
+    ctx.apply_repetition_penalty(y, off, hist, 1.05)
+    z = x.copy()
+    assert ref.apply_penalty(z, off, hist, 1.05) == 0
+    assert np.array_equal(y.view(U32), z.view(U32))

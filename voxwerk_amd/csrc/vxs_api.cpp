@@ -119,10 +119,9 @@ int check_shape(vxs_ctx* ctx, int rows, int vocab, const void* logits, int64_t l
     if (params_stride < 0) return fail(ctx, VXS_ERR_INVALID_ARG, "params_stride < 0");
     if (rows > 0 && (!logits || !params || !out_ids))
         return fail(ctx, VXS_ERR_INVALID_ARG, "null logits, params or out_ids");
-    if (vocab > vxs::kRowResidentMaxVocab)
+    if (vocab > vxs::kWideMaxVocab)
         return fail(ctx, VXS_ERR_UNSUPPORTED,
-                    "vocab " + std::to_string(vocab) + " exceeds the row-resident limit " +
-                        std::to_string(vxs::kRowResidentMaxVocab));
+                    "vocab " + std::to_string(vocab) + " exceeds the limit " + std::to_string(vxs::kWideMaxVocab));
     return VXS_OK;
 }
 

@@ -45,8 +45,11 @@ enum : int {
 constexpr int kRowResidentMaxVocab = 8192;
 // Largest vocabulary of the one-wave-per-row fast path (vxs_wave.h).
 constexpr int kWaveMaxVocab = 3072;
+// Largest vocabulary of the streaming kernel (vxs_wide.hip); its history bitmap lives in LDS.
+constexpr int kWideMaxVocab = 1 << 19;
 
 // Enqueue the sampler on `stream`. Returns hipSuccess or the launch error.
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream);
+hipError_t launch_sample_wide(const SampleArgs& a, hipStream_t stream);
 
 }  // namespace vxs

@@ -1207,7 +1207,8 @@ hipError_t launch_quad(const SampleArgs& a, int vec, hipStream_t stream) {
 
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream) {
     if (a.rows <= 0) return hipSuccess;
-    if (a.vocab <= 0 || a.vocab > kRowResidentMaxVocab) return hipErrorNotSupported;
+    if (a.vocab > kRowResidentMaxVocab) return launch_sample_wide(a, stream);
+    if (a.vocab <= 0) return hipErrorNotSupported;
     const int vec = (a.ld % 4 == 0) && (((uintptr_t)a.logits & 15u) == 0) ? 1 : 0;
     const int V = a.vocab;
     if (a.path == kPathQuad && V <= kWaveMaxVocab) {

@@ -1,0 +1,713 @@
+// vxs_wide.hip — the sampler for vocabularies above 8192 (up to 2^19), one 256-thread workgroup
+// per row, streaming the row from HBM instead of holding it in registers.
+//
+// Pass A reads the row once (16-byte loads, 1024 entries per sweep) and applies, per entry:
+//   S1 penalty      an LDS bitmap of the history ids marks the entries to rescale (s*rho, or the
+//                   correctly rounded s/rho); each distinct id once by construction  Sampler.cs:25-33
+//   S2 suppression  [supp_begin, supp_end) except keep_id, then ban_id -> -inf       TalkerGenerator.cs:247-248
+//   S3 greedy       running first-index argmax, no temperature                       Sampler.cs:37,90-95
+//   S4 temperature  x * fl32(1/T)                                                    Sampler.cs:39-40
+//   S5 top-k        (0 < k <= 256) a candidate buffer in LDS keeps every entry >= tau, where tau is
+//                   the k-th largest value seen so far: whenever the buffer fills, an exact radix
+//                   select finds the k-th largest buffered key, tau rises to it and the buffer is
+//                   compacted. tau never exceeds the row's k-th largest value, so the buffer ends
+//                   holding every entry the reference keeps.                        Sampler.cs:42-49
+// With at most 256 candidates left after the exact k-th largest, the reference's sequential fp64
+// arithmetic runs on them in index order (S6-S8, Sampler.cs:51-87) and the row is done after one
+// read. Any other row (top-k off or above 256, or ties overflowing the buffer) takes the general
+// path: a radix select of the k-th largest over the row, then a mass-weighted radix select of the
+// top-p cut over the fixed-point masses exp(d) (exact, order-independent sums, as in the other
+// kernels), ties at the cut resolved in index order, and an index-order draw; each step re-reads
+// the row (L2/HBM), so the general path costs several passes.
+#include <math.h>
+#include <stdint.h>
+
+#include "vxs_device.h"
+#include "vxs_internal.h"
+
+namespace vxs {
+namespace {
+
+using namespace dev;
+
+constexpr int kTW = 256;          // threads per row
+constexpr int kWW = kTW / 64;     // waves
+constexpr int kSweepW = 4 * kTW;  // entries per sweep
+constexpr int kCap = 2048;        // candidate buffer entries
+constexpr int kKMax = 256;        // largest top-k of the streaming path
+constexpr int kCandW = 256;       // exact-regime capacity
+constexpr int kRB = 256;          // radix buckets (8-bit digits)
+
+struct WideSmem {
+    uint32_t ckey[kCap];  // candidate keys (f2key of the value)
+    int32_t cidx[kCap];   // candidate indices
+    union {
+        uint32_t hcnt[kRB];
+        double hmass[kRB];
+    } h;
+    struct {
+        float cx[kCandW];
+        int32_t ci[kCandW];
+        double cp[kCandW];
+        int16_t cs[kCandW];
+    } ex;
+    uint64_t slot[4][kWW];
+    int32_t n;       // candidate count
+    int32_t err;
+    uint32_t tau_key;
+};
+
+// Workgroup combines that may be reused in a loop: a barrier before and after the slot read.
+struct BlkW {
+    int lane, wv, t;
+    WideSmem* s;
+    template <class Op>
+    __device__ __forceinline__ uint64_t combine(uint64_t w, Op op, int site = 0) const {
+        if (lane == 0) s->slot[site][wv] = w;
+        __syncthreads();
+        uint64_t r = s->slot[site][0];
+#pragma unroll
+        for (int i = 1; i < kWW; i++) r = op(r, s->slot[site][i]);
+        __syncthreads();
+        return r;
+    }
+    __device__ __forceinline__ uint32_t usum(uint32_t x) const {
+        return (uint32_t)combine(wave_sum(x), [](uint64_t p, uint64_t q) { return p + q; });
+    }
+    __device__ __forceinline__ double dsum(double x) const {
+        return __longlong_as_double((long long)combine((uint64_t)__double_as_longlong(wave_sum(x)),
+                                                       [](uint64_t p, uint64_t q) {
+                                                           return (uint64_t)__double_as_longlong(
+                                                               __longlong_as_double((long long)p) +
+                                                               __longlong_as_double((long long)q));
+                                                       }));
+    }
+    __device__ __forceinline__ uint32_t umax(uint32_t x) const {
+        return (uint32_t)combine(wave_umax(x), [](uint64_t p, uint64_t q) { return p > q ? p : q; });
+    }
+    __device__ __forceinline__ uint32_t umin(uint32_t x) const {
+        return (uint32_t)combine(wave_umin(x), [](uint64_t p, uint64_t q) { return p < q ? p : q; });
+    }
+    __device__ __forceinline__ bool any(bool p) const {
+        return combine(wave_any(p) ? 1u : 0u, [](uint64_t a, uint64_t b) { return a | b; }) != 0;
+    }
+    // exclusive prefix over threads; integer-valued doubles (exact)
+    __device__ __forceinline__ double excl(double v, double& total) const {
+        const double incl = wave_incl_sum(v);
+        if (lane == 0) s->slot[1][wv] = (uint64_t)__double_as_longlong(readlane_d(incl, 63));
+        __syncthreads();
+        double base = 0.0, tot = 0.0;
+#pragma unroll
+        for (int i = 0; i < kWW; i++) {
+            const double x = __longlong_as_double((long long)s->slot[1][i]);
+            base += i < wv ? x : 0.0;
+            tot += x;
+        }
+        __syncthreads();
+        total = tot;
+        return base + incl - v;
+    }
+    __device__ __forceinline__ uint32_t excl(uint32_t v, uint32_t& total) const {
+        const uint32_t incl = wave_incl_sum(v);
+        if (lane == 0) s->slot[1][wv] = readlane(incl, 63);
+        __syncthreads();
+        uint32_t base = 0, tot = 0;
+#pragma unroll
+        for (int i = 0; i < kWW; i++) {
+            const uint32_t x = (uint32_t)s->slot[1][i];
+            base += i < wv ? x : 0;
+            tot += x;
+        }
+        __syncthreads();
+        total = tot;
+        return base + incl - v;
+    }
+};
+
+// One row's transform of a raw logit: penalty, suppression, and (when sampling) temperature.
+struct RowX {
+    const uint32_t* bm;  // penalised-id bitmap (LDS) or null
+    float rho, rinv;
+    bool fastdiv;
+    int sb, se, keep, ban;
+    float invT;  // 1 for greedy rows
+    __device__ __forceinline__ float operator()(int i, float x) const {
+        if (bm && ((bm[i >> 5] >> (i & 31)) & 1u)) x = penalize(x, rho, rinv, fastdiv);
+        if ((i >= sb && i < se && i != keep) || i == ban) x = kNegInf;
+        return x * invT;
+    }
+};
+
+// Visits every entry of the row in index order groups: f(i, x) for the transformed value x of
+// entry i (i < V). Each thread handles 4 consecutive entries of every 1024-entry sweep.
+template <class F>
+__device__ __forceinline__ void for_row(const float* __restrict__ xrow, int V, int vec, int t, const RowX& X, F f) {
+    for (int base = 0; base < V; base += kSweepW) {
+        const int i0 = base + 4 * t;
+        float x[4];
+        if (vec && i0 + 3 < V) {
+            typedef float f4 __attribute__((ext_vector_type(4)));
+            const f4 q = __builtin_nontemporal_load((const f4*)(xrow + i0));
+            x[0] = q.x;
+            x[1] = q.y;
+            x[2] = q.z;
+            x[3] = q.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) x[j] = i0 + j < V ? xrow[i0 + j] : kNegInf;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (i0 + j < V) f(i0 + j, X(i0 + j, x[j]));
+    }
+}
+
+// k-th largest (1-based, with multiplicity) of the n buffered keys by an MSB-first radix select.
+__device__ __forceinline__ uint32_t buffer_kth(const BlkW& g, WideSmem& s, int n, int k) {
+    uint32_t prefix = 0, mask = 0;
+    int need = k;
+#pragma unroll 1
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int b = g.t; b < kRB; b += kTW) s.h.hcnt[b] = 0;
+        __syncthreads();
+        for (int j = g.t; j < n; j += kTW) {
+            const uint32_t key = s.ckey[j];
+            if ((key & mask) == prefix) atomicAdd(&s.h.hcnt[(key >> shift) & 0xff], 1u);
+        }
+        __syncthreads();
+        // thread b owns digit 255 - b: counts from the top
+        const uint32_t c = s.h.hcnt[kRB - 1 - g.t];
+        uint32_t tot;
+        const uint32_t above = g.excl(c, tot);  // entries with larger digits
+        int mine = -1;
+        if ((int)above < need && (int)(above + c) >= need) mine = kRB - 1 - g.t;
+        const uint32_t dg = g.umax((uint32_t)(mine + 1)) - 1;
+        const uint32_t ab = g.umax(mine >= 0 ? above + 1 : 0) - 1;
+        need -= (int)ab;
+        prefix |= dg << shift;
+        mask |= 0xffu << shift;
+    }
+    return prefix;
+}
+
+// Keep the buffered entries with key >= kmin (stable order). Returns the new count.
+__device__ __forceinline__ int buffer_filter(const BlkW& g, WideSmem& s, int n, uint32_t kmin) {
+    constexpr int kPer = kCap / kTW;
+    uint32_t kk[kPer];
+    int32_t ii[kPer];
+    uint32_t mine = 0;
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int j = g.t * kPer + q;
+        kk[q] = j < n ? s.ckey[j] : 0;
+        ii[q] = j < n ? s.cidx[j] : 0;
+        mine += (j < n && kk[q] >= kmin) ? 1u : 0u;
+    }
+    uint32_t tot;
+    uint32_t off = g.excl(mine, tot);  // its barriers order the reads before the writes below
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int j = g.t * kPer + q;
+        if (j < n && kk[q] >= kmin) {
+            s.ckey[off] = kk[q];
+            s.cidx[off] = ii[q];
+            off++;
+        }
+    }
+    __syncthreads();
+    return (int)tot;
+}
+
+// Exact regime on n <= kCandW candidates in index order (cx values, ci indices): the reference's
+// sequential fp64 arithmetic. Sequential phases run redundantly in every thread on LDS broadcasts.
+__device__ __forceinline__ int exact_block(const BlkW& g, WideSmem& s, int n, float m, bool topp, float top_p,
+                                           double u, double* prow) {
+    auto& ex = s.ex;
+    for (int j = g.t; j < n; j += kTW) ex.cp[j] = exp((double)(ex.cx[j] - m));  // Sampler.cs:57
+    __syncthreads();
+    double sum = 0.0;  // sequential in index order                                     :58
+    for (int j = 0; j < n; j++) sum += ex.cp[j];
+    __syncthreads();
+    for (int j = g.t; j < n; j += kTW) ex.cp[j] = ex.cp[j] / sum;  //                   :60
+    __syncthreads();
+    if (topp) {  //                                                                    :62-75
+        for (int j = g.t; j < n; j += kTW) {
+            const double pj = ex.cp[j];
+            int rank = 0;
+            for (int l = 0; l < n; l++) {
+                const double pl = ex.cp[l];
+                rank += (pl < pj) || (pl == pj && l < j);
+            }
+            ex.cs[rank] = (int16_t)j;
+        }
+        __syncthreads();
+        const double thr = (double)(1.0f - top_p);
+        double cum = 0.0;
+        int nrem = n - 1;  // the last sorted position is never removed (loop j < n - 1)
+        for (int q = 0; q < n - 1; q++) {
+            cum += ex.cp[ex.cs[q]];
+            if (!(cum <= thr)) {
+                nrem = q;
+                break;
+            }
+        }
+        __syncthreads();
+        for (int q = g.t; q < nrem; q += kTW) ex.cp[ex.cs[q]] = 0.0;
+        __syncthreads();
+        double s2 = 0.0;
+        for (int j = 0; j < n; j++) s2 += ex.cp[j];
+        __syncthreads();
+        for (int j = g.t; j < n; j += kTW) ex.cp[j] = ex.cp[j] / s2;
+        __syncthreads();
+    }
+    double acc = 0.0;  // inverse-CDF draw in index order                               :77-87
+    int last = 0, pick = -1;
+    for (int j = 0; j < n; j++) {
+        const double pj = ex.cp[j];
+        if (pj <= 0.0) continue;
+        acc += pj;
+        last = ex.ci[j];
+        if (u < acc) {
+            pick = last;
+            break;
+        }
+    }
+    if (prow)
+        for (int j = g.t; j < n; j += kTW) prow[ex.ci[j]] = ex.cp[j];
+    return pick >= 0 ? pick : last;
+}
+
+__global__ __launch_bounds__(kTW) void sample_wide_kernel(SampleArgs a, int vec) {
+    extern __shared__ uint32_t bm_dyn[];  // penalised-id bitmap, ceil(vocab / 32) words
+    __shared__ WideSmem s;
+    BlkW g;
+    g.t = threadIdx.x;
+    g.lane = g.t & 63;
+    g.wv = g.t >> 6;
+    g.s = &s;
+    const int r = blockIdx.x;
+    const int V = a.vocab;
+    const vxs_params P = a.params[(int64_t)r * a.params_stride];
+    const float* __restrict__ xrow = a.logits + (int64_t)r * a.ld;
+    float* orow = a.out_logits ? a.out_logits + (int64_t)r * V : nullptr;
+    double* prow = a.out_probs ? a.out_probs + (int64_t)r * V : nullptr;
+    const bool stop_pen = (a.kflags & KF_STOP_AFTER_PENALTY) != 0;
+
+    // ---- history bitmap (S1)
+    RowX X;
+    X.bm = nullptr;
+    X.rho = P.rep_penalty;
+    X.rinv = 1.0f / P.rep_penalty;
+    X.fastdiv = __builtin_fabsf(P.rep_penalty) >= 0x1p-60f && __builtin_fabsf(P.rep_penalty) <= 0x1p60f;
+    if (P.rep_penalty != 1.0f && a.hist_off != nullptr) {
+        const int words = (V + 31) >> 5;
+        for (int w = g.t; w < words; w += kTW) bm_dyn[w] = 0;
+        __syncthreads();
+        const int h0 = a.hist_off[r], h1 = a.hist_off[r + 1];
+        bool bad = false;
+        for (int h = h0 + g.t; h < h1; h += kTW) {
+            const int id = a.hist_ids[h];
+            if ((unsigned)id >= (unsigned)V) bad = true;
+            else atomicOr(&bm_dyn[id >> 5], 1u << (id & 31));
+        }
+        if (g.any(bad)) {
+            if (g.t == 0) a.out_ids[r] = VXS_ERR_ID_OUT_OF_RANGE;
+            return;
+        }
+        X.bm = bm_dyn;
+    }
+    if (stop_pen) {  // ApplyRepetitionPenalty alone: write the penalised row
+        RowX P1 = X;
+        P1.sb = P1.se = 0;
+        P1.keep = P1.ban = -1;
+        P1.invT = 1.0f;
+        for_row(xrow, V, vec, g.t, P1, [&](int i, float x) { orow[i] = x; });
+        if (g.t == 0) a.out_ids[r] = 0;
+        return;
+    }
+    X.sb = max(P.supp_begin, 0);
+    X.se = min(P.supp_end, V);
+    if (!(P.supp_begin < P.supp_end)) X.sb = X.se = 0;
+    X.keep = P.keep_id;
+    X.ban = P.ban_id;
+    const bool greedy = !P.do_sample;
+    X.invT = greedy ? 1.0f : (P.temperature == 1.0f ? 1.0f : 1.0f / P.temperature);
+
+    // ---- pass A: statistics, greedy argmax, streaming top-k candidates
+    const int K = P.top_k;
+    const bool kstream = !greedy && K > 0 && K <= kKMax && K < V;
+    bool collect = kstream;  // false once ties overflow the buffer (the general path takes over)
+    if (g.t == 0) {
+        s.n = 0;
+        s.tau_key = 0;  // below every real key: everything is a candidate until the buffer fills
+    }
+    __syncthreads();
+    float bv = kNegInf, tmx = kNegInf;
+    int bi = 0x7fffffff;
+    bool bad = false;
+    uint32_t fin = 0;
+    for (int base = 0; base < V; base += kSweepW) {
+        const int i0 = base + 4 * g.t;
+        float x[4];
+        if (vec && i0 + 3 < V) {
+            typedef float f4 __attribute__((ext_vector_type(4)));
+            const f4 q = __builtin_nontemporal_load((const f4*)(xrow + i0));
+            x[0] = q.x;
+            x[1] = q.y;
+            x[2] = q.z;
+            x[3] = q.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) x[j] = i0 + j < V ? xrow[i0 + j] : kNegInf;
+        }
+        const uint32_t tau = s.tau_key;
+        uint32_t keys[4];
+        bool cand[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = i0 + j;
+            cand[j] = false;
+            keys[j] = 0;
+            if (i >= V) continue;
+            const float v = X(i, x[j]);
+            if (greedy) {  // a thread's indices ascend: strict > keeps its first maximum
+                bad |= v != v;
+                if (v > bv || bi == 0x7fffffff) {
+                    bv = v;
+                    bi = i;
+                }
+                continue;
+            }
+            bad |= __builtin_amdgcn_class(v, 0x203);
+            tmx = fmaxf(tmx, v);
+            fin += v != kNegInf ? 1u : 0u;
+            if (collect && v != kNegInf) {
+                keys[j] = f2key(v);
+                cand[j] = keys[j] >= tau;
+            }
+        }
+        if (!collect) continue;
+        // append this sweep's candidates: per-wave compaction, one LDS atomic per wave
+        uint32_t mine = (uint32_t)cand[0] + cand[1] + cand[2] + cand[3];
+        const uint32_t incl = wave_incl_sum(mine);
+        const uint32_t wtot = readlane(incl, 63);
+        uint32_t wbase = 0;
+        if (g.lane == 63 && wtot) wbase = atomicAdd((uint32_t*)&s.n, wtot);
+        wbase = readlane(wbase, 63);
+        uint32_t pos = wbase + incl - mine;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (cand[j]) {
+                if (pos < (uint32_t)kCap) {
+                    s.ckey[pos] = keys[j];
+                    s.cidx[pos] = i0 + j;
+                }
+                pos++;
+            }
+        __syncthreads();
+        int n = s.n;
+        __syncthreads();  // every thread has read the count before the next sweep appends
+        if (n > kCap - kSweepW) {  // room for fewer than one sweep: raise tau and compact
+            const uint32_t kth = buffer_kth(g, s, n, K);
+            n = buffer_filter(g, s, n, kth);
+            if (g.t == 0) {
+                s.n = n;
+                s.tau_key = kth;
+            }
+            __syncthreads();
+            if (n > kCap - kSweepW) collect = false;  // ties fill the buffer: general path below
+        }
+    }
+    if (g.any(bad)) {
+        if (g.t == 0) a.out_ids[r] = VXS_ERR_NONFINITE;
+        return;
+    }
+    if (greedy) {
+        // first index of the maximum across the workgroup
+        const float wbv = wave_fmax(bv == bv ? bv : kNegInf);
+        int cand_i = (bv == wbv) ? bi : 0x7fffffff;
+        const uint32_t wbi = wave_umin((uint32_t)cand_i);
+        if (g.lane == 0) {
+            s.slot[2][g.wv] = __float_as_uint(wbv);
+            s.slot[3][g.wv] = wbi;
+        }
+        __syncthreads();
+        float best = __uint_as_float((uint32_t)s.slot[2][0]);
+        uint32_t besti = (uint32_t)s.slot[3][0];
+#pragma unroll
+        for (int w = 1; w < kWW; w++) {
+            const float ov = __uint_as_float((uint32_t)s.slot[2][w]);
+            const uint32_t oi = (uint32_t)s.slot[3][w];
+            if (ov > best || (ov == best && oi < besti)) {
+                best = ov;
+                besti = oi;
+            }
+        }
+        if (g.t == 0) a.out_ids[r] = (int)besti;
+        if (orow) for_row(xrow, V, vec, g.t, X, [&](int i, float x) { orow[i] = x; });
+        if (prow)
+            for (int i = g.t; i < V; i += kTW) prow[i] = 0.0;
+        return;
+    }
+    const float mx = key2f(g.umax(f2key(wave_fmax(tmx))));
+    const uint32_t cnt = g.usum(fin);
+    const double u = a.u ? a.u[r] : 0.0;
+    if (cnt == 0) {  // every entry -inf: the reference's draw returns the last id
+        if (g.t == 0) a.out_ids[r] = V - 1;
+        if (orow) for_row(xrow, V, vec, g.t, X, [&](int i, float x) { orow[i] = x; });
+        if (prow)
+            for (int i = g.t; i < V; i += kTW) prow[i] = __builtin_nan("");
+        return;
+    }
+
+    // ---- streaming top-k result: exact k-th largest of the buffer, then the exact regime
+    const bool topk_on = K > 0 && K < V && (uint32_t)K < cnt;
+    int n = s.n;
+    bool fast = collect;
+    uint32_t kthkey = 0;
+    if (fast && topk_on) {
+        kthkey = buffer_kth(g, s, n, K);
+        n = buffer_filter(g, s, n, kthkey);
+    } else if (fast) {
+        kthkey = 0;  // k >= finite entries: every finite entry is kept; the buffer holds them all
+    }
+    fast = fast && n <= kCandW;
+    float kth = topk_on ? key2f(kthkey) : kNegInf;
+    if (fast) {
+        // candidates into index order: rank by index
+        for (int j = g.t; j < n; j += kTW) {
+            const int ij = s.cidx[j];
+            int rank = 0;
+            for (int l = 0; l < n; l++) rank += s.cidx[l] < ij;
+            s.ex.cx[rank] = key2f(s.ckey[j]);
+            s.ex.ci[rank] = ij;
+        }
+        __syncthreads();
+        if (orow) for_row(xrow, V, vec, g.t, X, [&](int i, float x) { orow[i] = x < kth ? kNegInf : x; });
+        if (prow)
+            for (int i = g.t; i < V; i += kTW) prow[i] = 0.0;
+        __syncthreads();
+        const int id = exact_block(g, s, n, mx, P.top_p < 1.0f, P.top_p, u, prow);
+        if (g.t == 0) a.out_ids[r] = id;
+        return;
+    }
+
+    // =================== general path: several passes over the row ===================
+    // exact k-th largest over the whole row (radix select on keys), when top-k is active
+    if (topk_on) {
+        uint32_t prefix = 0, mask = 0;
+        int need = K;
+#pragma unroll 1
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            for (int b = g.t; b < kRB; b += kTW) s.h.hcnt[b] = 0;
+            __syncthreads();
+            for_row(xrow, V, vec, g.t, X, [&](int, float v) {
+                const uint32_t key = f2key(v);
+                if (v != kNegInf && (key & mask) == prefix) atomicAdd(&s.h.hcnt[(key >> shift) & 0xff], 1u);
+            });
+            __syncthreads();
+            const uint32_t c = s.h.hcnt[kRB - 1 - g.t];
+            uint32_t tot;
+            const uint32_t above = g.excl(c, tot);
+            int mine = -1;
+            if ((int)above < need && (int)(above + c) >= need) mine = kRB - 1 - g.t;
+            const uint32_t dg = g.umax((uint32_t)(mine + 1)) - 1;
+            const uint32_t ab = g.umax(mine >= 0 ? above + 1 : 0) - 1;
+            need -= (int)ab;
+            prefix |= dg << shift;
+            mask |= 0xffu << shift;
+        }
+        kth = key2f(prefix);
+    }
+    auto val = [&](int i, float x) -> float { return x < kth ? kNegInf : x; };  // top-k mask
+    if (orow) for_row(xrow, V, vec, g.t, X, [&](int i, float x) { orow[i] = val(i, x); });
+    // fixed-point masses of d = x - max
+    const int F = min(51, 53 - (32 - __clz(V - 1)));
+    const double scaleF = __builtin_ldexp(1.0, F);
+    auto wof = [&](float v) -> double { return fixed_point((double)exp_neg(v - mx), scaleF); };
+    float dc = kNegInf;  // cut: keep d > dc, or d == dc with index >= ic
+    int ic = 0;
+    double Skept;
+    if (P.top_p < 1.0f) {
+        // mass-weighted radix select over f2key(d): first entry in ascending (d, index) order whose
+        // inclusive cumulative mass exceeds T = floor(thr * S)
+        const double thr = (double)(1.0f - P.top_p);
+        uint32_t prefix = 0, mask = 0;
+        double below = 0.0, T = 0.0, S = 0.0;
+        bool last_only = false;
+#pragma unroll 1
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            for (int b = g.t; b < kRB; b += kTW) s.h.hmass[b] = 0.0;
+            __syncthreads();
+            for_row(xrow, V, vec, g.t, X, [&](int i, float x) {
+                const float v = val(i, x);
+                if (v == kNegInf) return;
+                const float d = v - mx;
+                const uint32_t key = f2key(d);
+                if ((key & mask) == prefix) atomicAdd(&s.h.hmass[(key >> shift) & 0xff], wof(v));
+            });
+            __syncthreads();
+            const double hb = s.h.hmass[g.t];  // thread b owns digit b (ascending)
+            double tot;
+            const double run = g.excl(hb, tot);
+            if (shift == 24) {
+                S = tot;
+                if (!(thr < 1.0)) {
+                    last_only = true;
+                    break;
+                }
+                T = floor(thr * S);
+                if (T >= S) {
+                    last_only = true;
+                    break;
+                }
+            }
+            const double rest = T - below;
+            int mine = -1;
+            if (run <= rest && rest - run < hb) mine = g.t;
+            const uint32_t dg = g.umax((uint32_t)(mine + 1)) - 1;
+            if (g.t == (int)dg) s.slot[0][0] = (uint64_t)__double_as_longlong(run);
+            __syncthreads();
+            below += __longlong_as_double((long long)s.slot[0][0]);
+            __syncthreads();
+            prefix |= dg << shift;
+            mask |= 0xffu << shift;
+        }
+        if (last_only) {
+            // the last entry in (d, index) order: the maximum with the highest index
+            int li = -1;
+            for_row(xrow, V, vec, g.t, X, [&](int i, float x) {
+                if (val(i, x) == mx) li = max(li, i);
+            });
+            ic = (int)g.umax((uint32_t)(li + 1)) - 1;
+            dc = 0.0f;
+            double wl = 0.0;
+            if (g.t == 0) wl = wof(mx);
+            below = S - g.dsum(wl);
+        } else {
+            // ties at the cut key: the crossing follows index order among them
+            dc = key2f(prefix);
+            ic = -1;
+            double run = below;
+            for (int base = 0; base < V && ic < 0; base += kSweepW) {
+                const int i0 = base + 4 * g.t;
+                double w4[4];
+                double mine = 0.0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int i = i0 + j;
+                    w4[j] = 0.0;
+                    if (i < V) {
+                        const float v = val(i, X(i, xrow[i]));
+                        if (v != kNegInf && v - mx == dc) w4[j] = wof(v);
+                    }
+                    mine += w4[j];
+                }
+                double tot;
+                const double ex0 = g.excl(mine, tot);
+                int hit = -1;
+                double hb = 0.0;
+                if (T >= run + ex0 && T - (run + ex0) < mine) {
+                    double acc = run + ex0;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        if (hit < 0 && w4[j] > 0.0 && T - acc < w4[j]) {
+                            hit = i0 + j;
+                            hb = acc;
+                        }
+                        acc += w4[j];
+                    }
+                }
+                const int h = (int)g.umax((uint32_t)(hit + 1)) - 1;
+                if (h >= 0) {
+                    if (hit == h) s.slot[0][0] = (uint64_t)__double_as_longlong(hb);
+                    __syncthreads();
+                    below = __longlong_as_double((long long)s.slot[0][0]);
+                    __syncthreads();
+                    ic = h;
+                }
+                run += tot;
+            }
+            if (ic < 0) ic = 0x7fffffff;  // unreachable for a crossing key range
+        }
+        Skept = S - below;
+    } else {
+        double ls = 0.0;
+        for_row(xrow, V, vec, g.t, X, [&](int i, float x) {
+            const float v = val(i, x);
+            if (v != kNegInf) ls += wof(v);
+        });
+        Skept = g.dsum(ls);
+    }
+    auto kept = [&](int i, float v) {
+        if (v == kNegInf) return false;
+        const float d = v - mx;
+        return d > dc || (d == dc && i >= ic);
+    };
+    // draw: first kept index whose inclusive prefix mass exceeds floor(u * Skept)
+    const double D = floor(u * Skept);
+    double run = 0.0;
+    int pick = -1;
+    for (int base = 0; base < V && pick < 0; base += kSweepW) {
+        const int i0 = base + 4 * g.t;
+        double w4[4];
+        double mine = 0.0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = i0 + j;
+            w4[j] = 0.0;
+            if (i < V) {
+                const float v = val(i, X(i, xrow[i]));
+                if (kept(i, v)) w4[j] = wof(v);
+            }
+            mine += w4[j];
+        }
+        double tot;
+        const double ex0 = g.excl(mine, tot);
+        int hit = -1;
+        if (D >= run + ex0 && D - (run + ex0) < mine) {
+            double acc = run + ex0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                acc += w4[j];
+                if (hit < 0 && w4[j] > 0.0 && D < acc) hit = i0 + j;
+            }
+        }
+        pick = (int)g.umax((uint32_t)(hit + 1)) - 1;
+        run += tot;
+    }
+    if (pick < 0) {  // no crossing: the last kept id with p > 0
+        int li = -1;
+        for_row(xrow, V, vec, g.t, X, [&](int i, float x) {
+            const float v = val(i, x);
+            if (kept(i, v) && v - mx >= -745.1331787109375f) li = max(li, i);
+        });
+        pick = max((int)g.umax((uint32_t)(li + 1)) - 1, 0);
+    }
+    if (g.t == 0) a.out_ids[r] = pick;
+    if (prow) {
+        double se = 0.0;
+        for_row(xrow, V, vec, g.t, X, [&](int i, float x) {
+            const float v = val(i, x);
+            if (kept(i, v)) se += (double)exp_neg(v - mx);
+        });
+        se = g.dsum(se);
+        for_row(xrow, V, vec, g.t, X, [&](int i, float x) {
+            const float v = val(i, x);
+            prow[i] = kept(i, v) ? (double)exp_neg(v - mx) / se : 0.0;
+        });
+    }
+}
+
+}  // namespace
+
+hipError_t launch_sample_wide(const SampleArgs& a, hipStream_t stream) {
+    if (a.rows <= 0) return hipSuccess;
+    if (a.vocab <= 0 || a.vocab > kWideMaxVocab) return hipErrorNotSupported;
+    const int vec = (a.ld % 4 == 0) && (((uintptr_t)a.logits & 15u) == 0) ? 1 : 0;
+    const size_t dyn = sizeof(uint32_t) * (size_t)((a.vocab + 31) / 32);
+    hipLaunchKernelGGL(sample_wide_kernel, dim3(a.rows), dim3(kTW), dyn, stream, a, vec);
+    return hipGetLastError();
+}
+
+}  // namespace vxs
