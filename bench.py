@@ -108,6 +108,52 @@ def summarize_pmc(path: str, copy_path: str, copy_mib: int) -> None:
                   f"calibrated ({len(vals)} dispatches)  {name[:90]}")
 
 
+def measure_device(ctx, w, steps: int, warmup: int, hip, np) -> dict:
+    """Kernel time of one workload with device-resident inputs rotated over enough copies to miss
+    the last-level cache; HIP events on the context stream."""
+    b = w.generate()
+    in_bytes = b.logits.nbytes + b.hist_ids.nbytes
+    nbuf = max(2, math.ceil(2 * LLC_BYTES / in_bytes) + 1)
+    d_logits = [hip.DeviceArray.from_numpy(b.logits)]
+    d_hist = [hip.DeviceArray.from_numpy(b.hist_ids)]
+    for _ in range(nbuf - 1):
+        a = hip.DeviceArray(b.logits.shape, np.float32)
+        a.copy_from(d_logits[0])
+        d_logits.append(a)
+        h = hip.DeviceArray(b.hist_ids.shape, np.int32)
+        h.copy_from(d_hist[0])
+        d_hist.append(h)
+    d_off = hip.DeviceArray.from_numpy(b.hist_off)
+    d_params = hip.DeviceArray.from_numpy(b.params[:1])
+    d_u = hip.DeviceArray.from_numpy(b.u)
+    d_ids = hip.DeviceArray((b.rows,), np.int32)
+
+    def step(i):
+        k = i % nbuf
+        ctx.sample_device(b.rows, w.vocab, d_logits[k], w.vocab, d_params, 0, d_u, d_ids, d_off, d_hist[k])
+
+    for i in range(warmup):
+        step(i)
+    hip.synchronize()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(ctx.stream())
+    for i in range(steps):
+        step(i)
+    e1.record(ctx.stream())
+    e1.synchronize()
+    us = e0.elapsed_ms(e1) / steps * 1e3
+    gbps = b.rows * w.bytes_per_row() / (us * 1e-6) / 1e9
+    step(0)
+    hip.synchronize()
+    ids = d_ids.numpy()
+    for a in d_logits + d_hist:
+        a.free()
+    return {"workload": f"{w.name} {b.rows}x{w.vocab}", "us_per_step": round(us, 3),
+            "rows_per_s": round(b.rows / (us * 1e-6), 1), "hbm_gbps": round(gbps, 1),
+            "hbm_pct_peak": round(100 * gbps / HBM_PEAK_GBPS, 2), "rotating_input_copies": nbuf, "_ids": ids,
+            "_batch": b}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -116,6 +162,8 @@ def main() -> int:
     ap.add_argument("--latency-steps", type=int, default=10000)
     ap.add_argument("--cpu-reps", type=int, default=15, help="passes of the CPU oracle over the batch")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
+    ap.add_argument("--no-extra", action="store_true", help="skip the other workloads (batched talker, wide vocab, "
+                                                             "code-predictor frame)")
     ap.add_argument("--summarize-trace", metavar="CSV")
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("COUNTER_CSV", "COPY_CSV", "COPY_MIB"),
                     help="per-kernel average of a rocprofv3 --pmc counter_collection.csv, calibrated by the "
@@ -246,6 +294,41 @@ def main() -> int:
         log(f"[bench] cpu oracle {cpu['value']:.0f} rows/s (1 thread), {cpu['all_cores']['value']:.0f} rows/s "
             f"({ncores} threads); parity {parity}")
 
+    extra = {}
+    if not args.no_extra:
+        # batched talker and wide vocabulary: device-resident kernel time
+        for wid, steps in ((3, 2000), (5, 100)):
+            m = measure_device(ctx, workloads.workload(wid), steps, max(10, steps // 10), hip, np)
+            b = m.pop("_batch")
+            ids = m.pop("_ids")
+            if not args.no_cpu:
+                from oracle import ref
+
+                rows = min(b.rows, 128)
+                o = ref.sample(b.logits[:rows], b.params[:rows], b.u[:rows], b.hist_off[:rows + 1], b.hist_ids,
+                               threads=os.cpu_count() or 1)
+                m["parity_first_rows"] = ref.classify(ids[:rows], o)
+            extra[workloads.NAMES[wid]] = m
+            log(f"[bench] {m['workload']}: {m['us_per_step']:.2f} us/step, {m['rows_per_s']:.4g} rows/s, "
+                f"{m['hbm_gbps']:.0f} GB/s")
+        # code-predictor frame: 15 dependent 16x2048 steps, host to host
+        w2 = workloads.workload(2)
+        steps2 = [w2.generate(step=k) for k in range(w2.steps)]
+        for _ in range(20):
+            for bb in steps2:
+                ctx.sample(bb.logits, bb.params, bb.u)
+        frames = []
+        for _ in range(200):
+            t = time.perf_counter_ns()
+            for bb in steps2:
+                ctx.sample(bb.logits, bb.params, bb.u)
+            frames.append(time.perf_counter_ns() - t)
+        frames = np.sort(np.array(frames)) / 1e3
+        extra[workloads.NAMES[2]] = {"workload": "code_predictor_frame 15 steps x 16x2048, host to host",
+                                     "us_per_frame_p50": round(float(frames[len(frames) // 2]), 2),
+                                     "us_per_step_p50": round(float(frames[len(frames) // 2]) / w2.steps, 2)}
+        log(f"[bench] code predictor frame: p50 {extra[workloads.NAMES[2]]['us_per_frame_p50']:.1f} us")
+
     traffic = read_traffic()
     out = {
         "metric": METRIC,
@@ -283,6 +366,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "parity": parity,
+        "other_workloads": extra,
     }
     print(json.dumps(out), flush=True)
     ctx.close()
