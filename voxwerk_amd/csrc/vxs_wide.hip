@@ -33,14 +33,15 @@ using namespace dev;
 constexpr int kTW = 256;          // threads per row
 constexpr int kWW = kTW / 64;     // waves
 constexpr int kSweepW = 4 * kTW;  // entries per sweep
-constexpr int kCap = 2048;        // candidate buffer entries
+constexpr int kCapW = 512;        // candidate buffer entries per wave
+constexpr int kPerL = kCapW / 64;  // ... per lane
 constexpr int kKMax = 256;        // largest top-k of the streaming path
 constexpr int kCandW = 256;       // exact-regime capacity
 constexpr int kRB = 256;          // radix buckets (8-bit digits)
 
 struct WideSmem {
-    uint32_t ckey[kCap];  // candidate keys (f2key of the value)
-    int32_t cidx[kCap];   // candidate indices
+    uint32_t wkey[kWW][kCapW];  // per-wave candidate keys (f2key of the value)
+    int32_t widx[kWW][kCapW];   // per-wave candidate indices
     union {
         uint32_t hcnt[kRB];
         double hmass[kRB];
@@ -52,9 +53,9 @@ struct WideSmem {
         int16_t cs[kCandW];
     } ex;
     uint64_t slot[4][kWW];
-    int32_t n;       // candidate count
-    int32_t err;
-    uint32_t tau_key;
+    int32_t wcnt[kWW];  // per-wave candidate counts after pass A (-1: the wave's buffer overflowed)
+    uint32_t tau_key;   // the largest k-th largest any wave has found so far (a shared lower bound)
+    int32_t n;          // exact-regime candidates
 };
 
 // Workgroup combines that may be reused in a loop: a barrier before and after the slot read.
@@ -162,60 +163,64 @@ __device__ __forceinline__ void for_row(const float* __restrict__ xrow, int V, i
     }
 }
 
-// k-th largest (1-based, with multiplicity) of the n buffered keys by an MSB-first radix select.
-__device__ __forceinline__ uint32_t buffer_kth(const BlkW& g, WideSmem& s, int n, int k) {
-    uint32_t prefix = 0, mask = 0;
-    int need = k;
-#pragma unroll 1
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int b = g.t; b < kRB; b += kTW) s.h.hcnt[b] = 0;
-        __syncthreads();
-        for (int j = g.t; j < n; j += kTW) {
-            const uint32_t key = s.ckey[j];
-            if ((key & mask) == prefix) atomicAdd(&s.h.hcnt[(key >> shift) & 0xff], 1u);
+// k-th largest (1-based, with multiplicity) of a wave's n >= k buffered keys: the largest key K
+// with at least k keys >= K, by bisection over [min key, max key]; wave-local, no LDS atomics.
+__device__ __forceinline__ uint32_t wave_kth(const uint32_t* keys, int lane, int n, int k) {
+    uint32_t kk[kPerL];
+    uint32_t lo = 0xffffffffu, hi = 0;
+#pragma unroll
+    for (int q = 0; q < kPerL; q++) {
+        const int j = lane + 64 * q;
+        kk[q] = j < n ? keys[j] : 0;
+        if (j < n) {
+            lo = min(lo, kk[q]);
+            hi = max(hi, kk[q]);
         }
-        __syncthreads();
-        // thread b owns digit 255 - b: counts from the top
-        const uint32_t c = s.h.hcnt[kRB - 1 - g.t];
-        uint32_t tot;
-        const uint32_t above = g.excl(c, tot);  // entries with larger digits
-        int mine = -1;
-        if ((int)above < need && (int)(above + c) >= need) mine = kRB - 1 - g.t;
-        const uint32_t dg = g.umax((uint32_t)(mine + 1)) - 1;
-        const uint32_t ab = g.umax(mine >= 0 ? above + 1 : 0) - 1;
-        need -= (int)ab;
-        prefix |= dg << shift;
-        mask |= 0xffu << shift;
     }
-    return prefix;
+    lo = wave_umin(lo);
+    hi = wave_umax(hi);
+#pragma unroll 1
+    while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo + 1) >> 1);
+        uint32_t c = 0;
+#pragma unroll
+        for (int q = 0; q < kPerL; q++) c += kk[q] >= mid ? 1u : 0u;  // empty slots hold 0 < mid
+        if ((int)wave_sum(c) >= k) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
 }
 
-// Keep the buffered entries with key >= kmin (stable order). Returns the new count.
-__device__ __forceinline__ int buffer_filter(const BlkW& g, WideSmem& s, int n, uint32_t kmin) {
-    constexpr int kPer = kCap / kTW;
-    uint32_t kk[kPer];
-    int32_t ii[kPer];
-    uint32_t mine = 0;
+// Keep a wave's buffered entries with key >= kmin (order kept). Returns the new count.
+__device__ __forceinline__ int wave_filter(uint32_t* keys, int32_t* idx, int lane, int n, uint32_t kmin) {
+    uint32_t kk[kPerL];
+    int32_t ii[kPerL];
 #pragma unroll
-    for (int q = 0; q < kPer; q++) {
-        const int j = g.t * kPer + q;
-        kk[q] = j < n ? s.ckey[j] : 0;
-        ii[q] = j < n ? s.cidx[j] : 0;
-        mine += (j < n && kk[q] >= kmin) ? 1u : 0u;
+    for (int q = 0; q < kPerL; q++) {
+        const int j = lane + 64 * q;
+        kk[q] = j < n ? keys[j] : 0;
+        ii[q] = j < n ? idx[j] : 0;
     }
-    uint32_t tot;
-    uint32_t off = g.excl(mine, tot);  // its barriers order the reads before the writes below
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint32_t m = 0;
 #pragma unroll
-    for (int q = 0; q < kPer; q++) {
-        const int j = g.t * kPer + q;
-        if (j < n && kk[q] >= kmin) {
-            s.ckey[off] = kk[q];
-            s.cidx[off] = ii[q];
-            off++;
+    for (int q = 0; q < kPerL; q++) {
+        const bool keep = lane + 64 * q < n && kk[q] >= kmin;
+        const uint64_t bal = __ballot(keep);
+        if (keep) {
+            const uint32_t pos = m + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+            keys[pos] = kk[q];
+            idx[pos] = ii[q];
         }
+        m += (uint32_t)__builtin_popcountll(bal);
     }
-    __syncthreads();
-    return (int)tot;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    return (int)m;
 }
 
 // Exact regime on n <= kCandW candidates in index order (cx values, ci indices): the reference's
@@ -332,101 +337,171 @@ __global__ __launch_bounds__(kTW) void sample_wide_kernel(SampleArgs a, int vec)
     X.ban = P.ban_id;
     const bool greedy = !P.do_sample;
     X.invT = greedy ? 1.0f : (P.temperature == 1.0f ? 1.0f : 1.0f / P.temperature);
+    if (g.t == 0) s.tau_key = 0;
+    __syncthreads();
 
-    // ---- pass A: statistics, greedy argmax, streaming top-k candidates
+    // ---- pass A: each wave streams its own quarter of the row (no workgroup barrier inside):
+    // statistics, greedy argmax and its own top-k candidate buffer. A wave's buffer keeps every
+    // entry >= the k-th largest the wave has seen, which never exceeds the row's k-th largest, so
+    // the four buffers together hold every entry the reference keeps.
     const int K = P.top_k;
     const bool kstream = !greedy && K > 0 && K <= kKMax && K < V;
-    bool collect = kstream;  // false once ties overflow the buffer (the general path takes over)
-    if (g.t == 0) {
-        s.n = 0;
-        s.tau_key = 0;  // below every real key: everything is a candidate until the buffer fills
-    }
-    __syncthreads();
-    float bv = kNegInf, tmx = kNegInf;
+    // With rho >= 1 the penalty never raises a value and with 1/T > 0 scaling keeps order, so an
+    // entry below tau before its penalty stays below after it: the penalty is then applied to the
+    // few candidates only. Otherwise every entry is penalised as it streams.
+    const bool pen_late = X.bm && P.rep_penalty >= 1.0f && X.invT > 0.0f && !greedy;
+    // wave-uniform switches (readfirstlane lets the compiler branch on them instead of masking)
+    const bool pen_each = __builtin_amdgcn_readfirstlane(X.bm != nullptr && !pen_late);
+    const bool supp_any = __builtin_amdgcn_readfirstlane(X.se > X.sb || X.ban >= 0);
+    const int Q = ((V + kTW * 4 - 1) / (kTW * 4)) * 256;  // a wave's range, a multiple of 256
+    const int lo = g.wv * Q, hi = min(V, lo + Q);
+    uint32_t* wkey = s.wkey[g.wv];
+    int32_t* widx = s.widx[g.wv];
+    bool collect = kstream;  // false once ties overflow the wave's buffer
+    int wn = 0;               // wave-uniform buffer fill
+    float tau = -3.402823466e38f;  // entries below tau are not candidates (-inf never is)
+    float bv = kNegInf, tmx = kNegInf, xmin = kPosInf;
     int bi = 0x7fffffff;
     bool bad = false;
-    uint32_t fin = 0;
-    for (int base = 0; base < V; base += kSweepW) {
-        const int i0 = base + 4 * g.t;
-        float x[4];
-        if (vec && i0 + 3 < V) {
-            typedef float f4 __attribute__((ext_vector_type(4)));
-            const f4 q = __builtin_nontemporal_load((const f4*)(xrow + i0));
-            x[0] = q.x;
-            x[1] = q.y;
-            x[2] = q.z;
-            x[3] = q.w;
-        } else {
+    uint32_t ninf = 0;  // wave-uniform count of -inf entries
+    // Raw buffer loads bounded by the row: lanes past its end read zeros instead of faulting, so
+    // every sweep is one branch-free 16-byte load per lane (entries at or past `hi` are masked).
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const __amdgpu_buffer_rsrc_t rowbuf =
+        __builtin_amdgcn_make_buffer_rsrc((void*)xrow, (short)0, V * (int)sizeof(float), 0x00020000);
+    auto load4 = [&](int base) -> f4 {
+        return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rowbuf, (base + 4 * g.lane) * 4, 0, 2));
+    };
+    // raw entries of one sweep -> values after penalty (unless deferred), suppression, temperature
+    auto prep = [&](int base, f4 q, float* x, float* v) {
+        const int i0 = base + 4 * g.lane;
+        x[0] = q.x;
+        x[1] = q.y;
+        x[2] = q.z;
+        x[3] = q.w;
 #pragma unroll
-            for (int j = 0; j < 4; j++) x[j] = i0 + j < V ? xrow[i0 + j] : kNegInf;
+        for (int j = 0; j < 4; j++) v[j] = x[j];
+        if (pen_each) {
+            const uint32_t word = X.bm[i0 >> 5];  // the 4 entries share one bitmap word
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if ((word >> ((i0 + j) & 31)) & 1u) v[j] = penalize(v[j], X.rho, X.rinv, X.fastdiv);
         }
-        const uint32_t tau = s.tau_key;
-        uint32_t keys[4];
+        if (supp_any &&
+            __builtin_amdgcn_readfirstlane((base < X.se && base + 256 > X.sb) || (X.ban >= base && X.ban < base + 256))) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = i0 + j;
+                if ((i >= X.sb && i < X.se && i != X.keep) || i == X.ban) v[j] = kNegInf;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] *= X.invT;
+        if (__builtin_amdgcn_readfirstlane(base + 256 > hi)) {  // the range's last sweep: mask its end
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = i0 + j < hi ? v[j] : kNegInf;
+        }
+    };
+    auto sweep_greedy = [&](int base, f4 q) {  // a lane's indices ascend: strict > keeps its first max
+        float x[4], v[4];
+        prep(base, q, x, v);
+        const int i0 = base + 4 * g.lane;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            bad |= v[j] != v[j];
+            const bool take = i0 + j < hi && (v[j] > bv || bi == 0x7fffffff);
+            bv = take ? v[j] : bv;
+            bi = take ? i0 + j : bi;
+        }
+    };
+    auto sweep_sample = [&](int base, f4 q) {
+        float x[4], v[4];
+        prep(base, q, x, v);
+        const int i0 = base + 4 * g.lane;
         bool cand[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int i = i0 + j;
-            cand[j] = false;
-            keys[j] = 0;
-            if (i >= V) continue;
-            const float v = X(i, x[j]);
-            if (greedy) {  // a thread's indices ascend: strict > keeps its first maximum
-                bad |= v != v;
-                if (v > bv || bi == 0x7fffffff) {
-                    bv = v;
-                    bi = i;
-                }
-                continue;
-            }
-            bad |= __builtin_amdgcn_class(v, 0x203);
-            tmx = fmaxf(tmx, v);
-            fin += v != kNegInf ? 1u : 0u;
-            if (collect && v != kNegInf) {
-                keys[j] = f2key(v);
-                cand[j] = keys[j] >= tau;
-            }
+            bad |= __builtin_amdgcn_class(v[j], 0x203);  // NaN or +inf
+            xmin = fminf(xmin, x[j]);
+            tmx = fmaxf(tmx, v[j]);
+            ninf += (uint32_t)__builtin_popcountll(__ballot(v[j] == kNegInf && i0 + j < hi));
+            cand[j] = v[j] >= tau;
         }
-        if (!collect) continue;
-        // append this sweep's candidates: per-wave compaction, one LDS atomic per wave
-        uint32_t mine = (uint32_t)cand[0] + cand[1] + cand[2] + cand[3];
-        const uint32_t incl = wave_incl_sum(mine);
-        const uint32_t wtot = readlane(incl, 63);
-        uint32_t wbase = 0;
-        if (g.lane == 63 && wtot) wbase = atomicAdd((uint32_t*)&s.n, wtot);
-        wbase = readlane(wbase, 63);
-        uint32_t pos = wbase + incl - mine;
+        if (!collect) return;
+        if (!__ballot(cand[0] || cand[1] || cand[2] || cand[3])) return;
+        // another wave may have raised the shared bound: use it too
+        const float ts = key2f(__hip_atomic_load(&s.tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        if (ts > tau) {
+            tau = ts;
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (cand[j]) {
-                if (pos < (uint32_t)kCap) {
-                    s.ckey[pos] = keys[j];
-                    s.cidx[pos] = i0 + j;
-                }
-                pos++;
-            }
-        __syncthreads();
-        int n = s.n;
-        __syncthreads();  // every thread has read the count before the next sweep appends
-        if (n > kCap - kSweepW) {  // room for fewer than one sweep: raise tau and compact
-            const uint32_t kth = buffer_kth(g, s, n, K);
-            n = buffer_filter(g, s, n, kth);
-            if (g.t == 0) {
-                s.n = n;
-                s.tau_key = kth;
-            }
-            __syncthreads();
-            if (n > kCap - kSweepW) collect = false;  // ties fill the buffer: general path below
+            for (int j = 0; j < 4; j++) cand[j] = cand[j] && v[j] >= tau;
         }
-    }
+        if (pen_late) {  // the candidates' exact values
+            const uint32_t word = X.bm[i0 >> 5];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (cand[j] && ((word >> ((i0 + j) & 31)) & 1u)) {
+                    v[j] = penalize(x[j], X.rho, X.rinv, X.fastdiv) * X.invT;
+                    cand[j] = v[j] >= tau;
+                }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const bool c = collect && cand[j] && v[j] >= tau;
+            const uint64_t bal = __ballot(c);
+            if (bal) {
+                if (c) {
+                    const uint32_t pos = (uint32_t)wn + __builtin_amdgcn_mbcnt_hi(
+                                                            (uint32_t)(bal >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+                    wkey[pos] = f2key(v[j]);
+                    widx[pos] = i0 + j;
+                }
+                wn += __builtin_popcountll(bal);
+                if (wn > kCapW - 64) {  // room for less than one more slot: raise tau and compact
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    const uint32_t kth = wave_kth(wkey, g.lane, wn, K);
+                    wn = wave_filter(wkey, widx, g.lane, wn, kth);
+                    tau = fmaxf(tau, key2f(kth));
+                    if (g.lane == 0) atomicMax(&s.tau_key, kth);
+                    if (wn > kCapW - 64) collect = false;  // ties: the general path below
+                }
+            }
+        }
+    };
+    // kPF sweeps in flight per lane: the next group's loads are issued before this group is used
+    // (loads past the row return zeros, so they are issued unconditionally: no branch around a
+    // load keeps the wait counters exact)
+    constexpr int kPF = 8;
+    auto stream = [&](auto sweep) {
+        f4 cur[kPF];
+#pragma unroll
+        for (int q = 0; q < kPF; q++) cur[q] = load4(lo + q * 256);
+        for (int gb = lo; gb < hi; gb += kPF * 256) {
+            f4 nxt[kPF];
+#pragma unroll
+            for (int q = 0; q < kPF; q++) nxt[q] = load4(gb + (kPF + q) * 256);
+#pragma unroll
+            for (int q = 0; q < kPF; q++)
+                if (gb + q * 256 < hi) sweep(gb + q * 256, cur[q]);
+#pragma unroll
+            for (int q = 0; q < kPF; q++) cur[q] = nxt[q];
+        }
+    };
+    if (greedy) stream(sweep_greedy);
+    else stream(sweep_sample);
+    const bool huge = xmin < -1.0e37f;  // a deferred penalty might overflow such a value to -inf
+    if (g.lane == 0) s.wcnt[g.wv] = collect ? wn : -1;
     if (g.any(bad)) {
         if (g.t == 0) a.out_ids[r] = VXS_ERR_NONFINITE;
         return;
     }
     if (greedy) {
-        // first index of the maximum across the workgroup
-        const float wbv = wave_fmax(bv == bv ? bv : kNegInf);
-        int cand_i = (bv == wbv) ? bi : 0x7fffffff;
-        const uint32_t wbi = wave_umin((uint32_t)cand_i);
+        // first index of the maximum across the workgroup (wave ranges ascend in index)
+        const float wbv = wave_fmax(bv);
+        const uint32_t wbi = wave_umin(bv == wbv ? (uint32_t)bi : 0xffffffffu);
         if (g.lane == 0) {
             s.slot[2][g.wv] = __float_as_uint(wbv);
             s.slot[3][g.wv] = wbi;
@@ -449,8 +524,23 @@ __global__ __launch_bounds__(kTW) void sample_wide_kernel(SampleArgs a, int vec)
             for (int i = g.t; i < V; i += kTW) prow[i] = 0.0;
         return;
     }
-    const float mx = key2f(g.umax(f2key(wave_fmax(tmx))));
-    const uint32_t cnt = g.usum(fin);
+    // Statistics of pass A are exact unless the penalty was deferred to candidates: then the max
+    // comes from the candidates (the maximum is always one) and, if a penalty could overflow a
+    // value to -inf, the general path recounts with the full transform.
+    float mx = key2f(g.umax(f2key(wave_fmax(tmx))));
+    uint32_t cnt = (uint32_t)V -
+                   (uint32_t)g.combine(g.lane == 0 ? ninf : 0u, [](uint64_t p, uint64_t q) { return p + q; });
+    const bool restat = pen_late && g.any(huge);
+    if (restat) {
+        float m2 = kNegInf;
+        uint32_t c2 = 0;
+        for_row(xrow, V, vec, g.t, X, [&](int, float v) {
+            m2 = fmaxf(m2, v);
+            c2 += v != kNegInf ? 1u : 0u;
+        });
+        mx = key2f(g.umax(f2key(wave_fmax(m2))));
+        cnt = g.usum(c2);
+    }
     const double u = a.u ? a.u[r] : 0.0;
     if (cnt == 0) {  // every entry -inf: the reference's draw returns the last id
         if (g.t == 0) a.out_ids[r] = V - 1;
@@ -460,39 +550,95 @@ __global__ __launch_bounds__(kTW) void sample_wide_kernel(SampleArgs a, int vec)
         return;
     }
 
-    // ---- streaming top-k result: exact k-th largest of the buffer, then the exact regime
+    // ---- streaming top-k result: exact k-th largest over the four buffers, then the exact regime
     const bool topk_on = K > 0 && K < V && (uint32_t)K < cnt;
-    int n = s.n;
-    bool fast = collect;
-    uint32_t kthkey = 0;
-    if (fast && topk_on) {
-        kthkey = buffer_kth(g, s, n, K);
-        n = buffer_filter(g, s, n, kthkey);
-    } else if (fast) {
-        kthkey = 0;  // k >= finite entries: every finite entry is kept; the buffer holds them all
-    }
-    fast = fast && n <= kCandW;
-    float kth = topk_on ? key2f(kthkey) : kNegInf;
+    bool fast = kstream && !restat;
+#pragma unroll
+    for (int w = 0; w < kWW; w++) fast = fast && s.wcnt[w] >= 0;
+    float kth = kNegInf;
     if (fast) {
-        // candidates into index order: rank by index
-        for (int j = g.t; j < n; j += kTW) {
-            const int ij = s.cidx[j];
-            int rank = 0;
-            for (int l = 0; l < n; l++) rank += s.cidx[l] < ij;
-            s.ex.cx[rank] = key2f(s.ckey[j]);
-            s.ex.ci[rank] = ij;
+        int wc[kWW];
+#pragma unroll
+        for (int w = 0; w < kWW; w++) wc[w] = s.wcnt[w];
+        // thread t looks at entries t, t+256, ... of the concatenated buffers
+        auto valid = [&](int j) { return (j % kCapW) < wc[j / kCapW]; };
+        const uint32_t* keys = &s.wkey[0][0];
+        const int32_t* idxs = &s.widx[0][0];
+        uint32_t kthkey = 0;
+        if (topk_on) {  // radix select over the union
+            uint32_t prefix = 0, mask = 0;
+            int need = K;
+#pragma unroll 1
+            for (int shift = 24; shift >= 0; shift -= 8) {
+                for (int b = g.t; b < kRB; b += kTW) s.h.hcnt[b] = 0;
+                __syncthreads();
+                for (int j = g.t; j < kWW * kCapW; j += kTW)
+                    if (valid(j) && (keys[j] & mask) == prefix) atomicAdd(&s.h.hcnt[(keys[j] >> shift) & 0xff], 1u);
+                __syncthreads();
+                const uint32_t c = s.h.hcnt[kRB - 1 - g.t];
+                uint32_t tot;
+                const uint32_t above = g.excl(c, tot);
+                int mine = -1;
+                if ((int)above < need && (int)(above + c) >= need) mine = kRB - 1 - g.t;
+                const uint32_t dg = g.umax((uint32_t)(mine + 1)) - 1;
+                const uint32_t ab = g.umax(mine >= 0 ? above + 1 : 0) - 1;
+                need -= (int)ab;
+                prefix |= dg << shift;
+                mask |= 0xffu << shift;
+            }
+            kthkey = prefix;
+            kth = key2f(kthkey);
         }
+        if (pen_late) {  // the exact maximum: the largest candidate
+            uint32_t km = 0;
+            for (int j = g.t; j < kWW * kCapW; j += kTW)
+                if (valid(j)) km = max(km, keys[j]);
+            mx = key2f(g.umax(km));
+        }
+        // the candidates (key >= kth) into the exact-regime arrays, then index order
+        if (g.t == 0) s.n = 0;
         __syncthreads();
-        if (orow) for_row(xrow, V, vec, g.t, X, [&](int i, float x) { orow[i] = x < kth ? kNegInf : x; });
-        if (prow)
-            for (int i = g.t; i < V; i += kTW) prow[i] = 0.0;
+        for (int j = g.t; j < kWW * kCapW; j += kTW)
+            if (valid(j) && keys[j] >= kthkey) {
+                const int q = atomicAdd(&s.n, 1);
+                if (q < kCandW) {
+                    s.ex.ci[q] = idxs[j];
+                    s.ex.cx[q] = key2f(keys[j]);
+                }
+            }
         __syncthreads();
-        const int id = exact_block(g, s, n, mx, P.top_p < 1.0f, P.top_p, u, prow);
-        if (g.t == 0) a.out_ids[r] = id;
-        return;
+        const int n = s.n;
+        if (n <= kCandW) {
+            int ij = 0;
+            float xj = 0.0f;
+            if (g.t < n) {
+                ij = s.ex.ci[g.t];
+                xj = s.ex.cx[g.t];
+            }
+            int rank = 0;
+            for (int l = 0; l < n; l++) rank += s.ex.ci[l] < ij;
+            __syncthreads();
+            if (g.t < n) {
+                s.ex.ci[rank] = ij;
+                s.ex.cx[rank] = xj;
+            }
+            __syncthreads();
+            if (orow) for_row(xrow, V, vec, g.t, X, [&](int i, float x) { orow[i] = x < kth ? kNegInf : x; });
+            if (prow)
+                for (int i = g.t; i < V; i += kTW) prow[i] = 0.0;
+            __syncthreads();
+            const int id = exact_block(g, s, n, mx, P.top_p < 1.0f, P.top_p, u, prow);
+            if (g.t == 0) a.out_ids[r] = id;
+            return;
+        }
     }
 
     // =================== general path: several passes over the row ===================
+    if (pen_late && !restat) {  // the exact maximum with the full transform
+        float m2 = kNegInf;
+        for_row(xrow, V, vec, g.t, X, [&](int, float v) { m2 = fmaxf(m2, v); });
+        mx = key2f(g.umax(f2key(wave_fmax(m2))));
+    }
     // exact k-th largest over the whole row (radix select on keys), when top-k is active
     if (topk_on) {
         uint32_t prefix = 0, mask = 0;
