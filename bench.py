@@ -304,10 +304,10 @@ def main() -> int:
             if not args.no_cpu:
                 from oracle import ref
 
-                rows = min(b.rows, 128)
-                o = ref.sample(b.logits[:rows], b.params[:rows], b.u[:rows], b.hist_off[:rows + 1], b.hist_ids,
+                nchk = min(b.rows, 128)
+                o = ref.sample(b.logits[:nchk], b.params[:nchk], b.u[:nchk], b.hist_off[:nchk + 1], b.hist_ids,
                                threads=os.cpu_count() or 1)
-                m["parity_first_rows"] = ref.classify(ids[:rows], o)
+                m["parity_first_rows"] = ref.classify(ids[:nchk], o)
             extra[workloads.NAMES[wid]] = m
             log(f"[bench] {m['workload']}: {m['us_per_step']:.2f} us/step, {m['rows_per_s']:.4g} rows/s, "
                 f"{m['hbm_gbps']:.0f} GB/s")

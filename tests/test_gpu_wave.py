@@ -104,3 +104,39 @@ def test_wave_history_errors(ctx):
     ids = ctx.sample(x, p, np.full(1024, 0.5), off, hist, path="wave", raise_on_error=False)
     assert ids[3] == -2 and ids[50] == -2
     assert (np.delete(ids, [3, 50]) >= 0).all()
+
+
+def test_wave_equal_mass_cuts(ctx):
+    """Top-p cuts that fall inside a group of equal logits (equal masses): the wave path keeps the
+    group's higher indices where equal masses imply equal logits (logits 4 to 11 below the max) and
+    hands the row back elsewhere; groups of logits one ulp apart near the max share masses without
+    sharing logits, which only the general path orders correctly."""
+    vocab = 3072
+    rng = np.random.default_rng(77)
+    rows = 48
+    x = np.full((rows, vocab), -np.inf, np.float32)
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = 1
+    p["temperature"] = 1.0
+    p["rep_penalty"] = 1.0
+    p["keep_id"] = -1
+    p["ban_id"] = -1
+    for r in range(rows):
+        pos = rng.permutation(vocab)
+        x[r, pos[:400]] = rng.uniform(-14.0, -9.0, 400).astype(np.float32)  # background
+        x[r, pos[400]] = 0.0                                                  # the max
+        kind = r % 3
+        group = pos[401:441]
+        if kind == 0:    # equal logits 5 below the max: handled by the wave path
+            x[r, group] = np.float32(-5.0)
+            p["top_p"][r] = 0.9
+        elif kind == 1:  # equal logits 2 below the max: masses outside the safe range
+            x[r, group] = np.float32(-2.0)
+            p["top_p"][r] = 0.8
+        else:            # logits one ulp apart 0.3 below the max: equal masses, distinct logits
+            base = np.float32(-0.3)
+            x[r, group] = np.nextafter(np.full(40, base), np.float32(0.0)).astype(np.float32)
+            x[r, group[::2]] = base
+            p["top_p"][r] = 0.6
+    u = rng.random(rows)
+    run_both_paths(ctx, x, p, u, label="equal-mass cuts")

@@ -53,6 +53,16 @@ def build_hip() -> str:
     return out
 
 
+def build_selfcheck() -> str:
+    """Exhaustive device check of the fp32 exponential the one-wave path relies on (run by a GPU test)."""
+    os.makedirs(LIB, exist_ok=True)
+    out = os.path.join(LIB, "vxs_selfcheck")
+    flags = [f for f in HIP_FLAGS if f != "-fPIC"]
+    _run([HIPCC, *flags, f"-I{CSRC}", "-o", out + ".tmp", os.path.join(CSRC, "vxs_selfcheck.hip")])
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build_synth() -> str:
     os.makedirs(LIB, exist_ok=True)
     out = os.path.join(LIB, "libvxs_synth.so")
@@ -75,6 +85,7 @@ def build_all(with_tests: bool = True) -> None:
         raise RuntimeError("hipcc not found: a ROCm toolchain is required")
     build_synth()
     build_hip()
+    build_selfcheck()
     if with_tests and os.path.exists(os.path.join(REPO, "tests", "cpp", "test_facade.cpp")):
         build_facade_test()
 

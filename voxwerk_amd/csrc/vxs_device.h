@@ -20,6 +20,8 @@ enum : int {
     kRowShr8 = 0x118,
     kRowBcast15 = 0x142,
     kRowBcast31 = 0x143,
+    kQuadSwap1 = 0xb1,  // quad_perm [1,0,3,2]
+    kQuadSwap2 = 0x4e,  // quad_perm [2,3,0,1]
 };
 
 // Lane value moved by DPP; lanes whose source is outside the row/mask keep `old`.
@@ -73,6 +75,22 @@ __device__ __forceinline__ double wave_incl_sum(double x) {
     VXS_FSTEP(kRowBcast15, 0xa)
     VXS_FSTEP(kRowBcast31, 0xc)
 #undef VXS_FSTEP
+    return x;
+}
+// Inclusive prefix sum inside each row of 16 lanes.
+__device__ __forceinline__ double row_incl_sum(double x) {
+#define VXS_FSTEP(C) x += __longlong_as_double((long long)dpp64<C>(0, (uint64_t)__double_as_longlong(x)));
+    VXS_FSTEP(kRowShr1)
+    VXS_FSTEP(kRowShr2)
+    VXS_FSTEP(kRowShr4)
+    VXS_FSTEP(kRowShr8)
+#undef VXS_FSTEP
+    return x;
+}
+// Sum over each quad of lanes, in every lane of the quad.
+__device__ __forceinline__ double quad_sum(double x) {
+    x += __longlong_as_double((long long)dpp64<kQuadSwap1>(0, (uint64_t)__double_as_longlong(x)));
+    x += __longlong_as_double((long long)dpp64<kQuadSwap2>(0, (uint64_t)__double_as_longlong(x)));
     return x;
 }
 __device__ __forceinline__ double readlane_d(double x, int lane) {
@@ -190,12 +208,14 @@ __device__ __forceinline__ float key2f(uint32_t k) {
     return __uint_as_float(u);
 }
 
-// round(e * 2^F) as an integer-valued double, for 0 <= e * 2^F < 2^52. Masses in this form add
-// exactly (every partial sum stays an integer below 2^53), so sums and LDS atomics are
-// order-independent.
-__device__ __forceinline__ double fixed_point(double e, double scale) {
-    return __builtin_fma(e, scale, 4503599627370496.0) - 4503599627370496.0;
-}
+// Nucleus mass of a weight q in [0, 1]: fl32(fl32(q + Cb) - Cb) with Cb = 2^(23 - F), a multiple of
+// 2^-F within 1.5 ulp of q (fl32(q + Cb) >= Cb has an ulp of at least 2^-F; below Cb the subtraction
+// is exact, and every fp32 value at or above Cb is a multiple of 2^-F). Sums of up to 2^(53-F) such
+// masses are exact in double precision, so partial sums and LDS atomics are order-independent.
+__device__ __forceinline__ float mass_bias(int F) { return __uint_as_float((uint32_t)(150 - F) << 23); }
+__device__ __forceinline__ float mass_of(float q, float Cb) { return (q + Cb) - Cb; }
+// The same mass as an integer-valued double (units of 2^-F).
+__device__ __forceinline__ double fixed_mass(float q, float Cb, double scaleF) { return (double)mass_of(q, Cb) * scaleF; }
 
 // Repetition penalty of one logit (Sampler.cs:31): s*rho if s < 0, else s/rho correctly rounded.
 // The quotient uses rinv = RN(1/rho) and one fma correction (Markstein): with s and rho in

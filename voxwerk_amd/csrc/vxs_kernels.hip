@@ -845,6 +845,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
     // F fraction bits: vocab * 2^F <= 2^53 (exact double sums) and e * 2^F < 2^52.
     const int F = min(51, 53 - (32 - __clz(V - 1)));
     const double scaleF = __builtin_ldexp(1.0, F);
+    const float Cb = mass_bias(F);
 #pragma unroll
     for (int e = 0; e < NE; e++) v[e] = v[e] - m;  // d = x - max; -inf stays -inf
     // Masses and keys are recomputed where they are needed (a few VALU ops) instead of being kept
@@ -852,7 +853,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
     auto qof = [&](int e) -> double {
         float x = v[e];
         asm volatile("" : "+v"(x));
-        return fixed_point((double)exp_neg(x), scaleF);
+        return fixed_mass(exp_neg(x), Cb, scaleF);
     };
     auto keyof = [&](int e) -> uint32_t {
         float x = v[e];
@@ -877,7 +878,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
         };
 #pragma unroll
         for (int e = 0; e < NE; e++)  // -inf entries add 0 to bucket 0
-            atomicAdd(&sm.u.nh[e >> 2][bk(e)], fixed_point((double)exp_neg(v[e]), scaleF));
+            atomicAdd(&sm.u.nh[e >> 2][bk(e)], fixed_mass(exp_neg(v[e]), Cb, scaleF));
         if (g.t == 0) {
             sm.ctl.bstar = -1;
             sm.ctl.list_n = 0;
@@ -1071,7 +1072,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
         for (int c = 0; c < NC; c++) {
             double s2 = 0.0;
 #pragma unroll
-            for (int j = 0; j < 4; j++) s2 += fixed_point((double)exp_neg(v[c * 4 + j]), scaleF);
+            for (int j = 0; j < 4; j++) s2 += fixed_mass(exp_neg(v[c * 4 + j]), Cb, scaleF);
             const double w = wave_sum(s2);
             if (g.lane == 0) g.slot[kSiteChunk0 + c][g.wv] = (uint64_t)__double_as_longlong(w);
         }

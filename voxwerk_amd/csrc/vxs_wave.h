@@ -1,14 +1,16 @@
 // vxs_wave.h — the one-wave fast path of the sampler (vocabularies up to 3072).
 //
 // One wave64 owns a row: lane l holds elements c*256 + 4l + j of sweep c, loaded once from HBM and
-// kept in VGPRs to the sampled id. Every reduction, scan and select is wave-local (DPP, readlane,
-// ballot); LDS holds the penalty staging, one histogram and a short ranking list, small enough
-// for 16 rows per CU. The path covers what full-vocabulary sampling needs — penalty, suppression,
-// greedy, temperature, the nucleus regime with or without top-p — and hands a row back untouched
-// (return value 1) when it needs the general algorithm: an active top-k, a history longer than
-// 512 ids, at most 256 candidates (the exact regime), a top-p cut whose crossing bucket holds more
-// than 64 entries or is not found, a draw that finds no crossing, or a call that asks for the
-// write-back logits or the probabilities. Every decision depends on the row alone, so results do not depend on the batch.
+// kept in VGPRs to the sampled id (first the logits, then their nucleus masses). Every reduction,
+// scan and select is wave-local (DPP, readlane, ballot); LDS holds the penalty staging, one
+// histogram and a short ranking list, small enough for 16 rows per CU. The path covers what
+// full-vocabulary sampling needs — penalty, suppression, greedy, temperature, the nucleus regime
+// with or without top-p — and hands a row back untouched (return value 1) when it needs the general
+// algorithm: an active top-k, a history longer than 512 ids, at most 256 candidates (the exact
+// regime), a top-p cut whose crossing bucket holds more than 64 entries, a cut inside a group of
+// equal masses far from where equal masses imply equal logits, a draw that finds no crossing, or a
+// call that asks for the write-back logits or the probabilities. Every decision depends on the row
+// alone, so results do not depend on the batch.
 //
 //   S1 penalty      the row is staged into LDS in parts of up to 6 sweeps; the wave reads the
 //                   original logit of every history id of the part, then writes s*rho or the
@@ -17,13 +19,14 @@
 //   S2 suppression  [supp_begin, supp_end) except keep_id, then ban_id -> -inf  TalkerGenerator.cs:247-248
 //   S3 greedy       first index of the max, no temperature                      Sampler.cs:37,90-95
 //   S4 temperature  x * fl32(1/T)                                               Sampler.cs:39-40
-//   S6-S8 nucleus   fp32 masses exp(d), d = x - max, rounded to multiples of 2^-F as integer-valued
-//                   doubles (exact, order-independent sums). A histogram of the masses over d
-//                   (512 LDS buckets) gives the total and the bucket where the ascending
-//                   cumulative mass crosses floor(fl32(1 - top_p) * total); that bucket's entries
-//                   are ranked by (d, index) for the exact cut. The draw scans the kept masses in
-//                   index order a sweep at a time and stops in the sweep holding
-//                   floor(u * kept mass).                                       Sampler.cs:51-87
+//   S6-S8 nucleus   fp32 masses exp(d), d = x - max, rounded to multiples of 2^-F (exact,
+//                   order-independent double sums); the masses replace the logits in VGPRs.
+//                   A histogram over the top bits of the masses (1024 LDS buckets, a log scale)
+//                   gives the total and the bucket where the ascending cumulative mass crosses
+//                   floor(fl32(1 - top_p) * total); that bucket's entries are ranked by
+//                   (mass, index) for the exact cut. The draw sums the kept masses per sweep,
+//                   finds the sweep, then the lane, then the entry holding
+//                   floor(u * kept mass) in index order.                        Sampler.cs:51-87
 #pragma once
 
 #include <stdint.h>
@@ -38,18 +41,19 @@ using namespace dev;
 
 constexpr int kSweep = 256;  // elements per sweep: 64 lanes x 4
 constexpr int kPart = 6;     // sweeps staged in LDS at once for the penalty
-constexpr int kNB = 512;     // top-p histogram buckets (8 per lane)
+constexpr int kNB = 1024;    // top-p histogram buckets (16 per lane)
 constexpr int kBPL = kNB / 64;
 constexpr int kL = 64;       // crossing-bucket entries ranked exactly (one per lane)
 constexpr int kExact = 256;  // rows with at most this many candidates take the exact regime
 constexpr int kHP = 8;       // history ids per lane fetched with the row (512 per row)
 
+typedef double dbl2 __attribute__((ext_vector_type(2)));
+
 struct Sel {
-    double hist[kNB];
-    uint32_t key[kL];
-    int32_t idx[kL];
-    double ws[kL];
-    int32_t at[kL];
+    alignas(16) double hist[kNB];       // mass per bucket; then the draw's per-lane sweep sums
+    uint64_t key[kL + 4];   // crossing-bucket entries: mass bits << 32 | index, then 4 pads
+    uint64_t skey[kL];      // the same in rank order
+    double ws[kL];          // their masses in rank order
 };
 
 // LDS ordering inside one wave.
@@ -217,28 +221,29 @@ __device__ __forceinline__ int wave_fast_row(const SampleArgs& a, int vec, int r
         return 0;
     }
 
-    // ---- S4: temperature (always multiplied: x * 1 is x), and the finite-input contract
+    // ---- S4: temperature (x * 1 is x, so the common T = 1 skips the pass)
     const float invT = P.temperature == 1.0f ? 1.0f : 1.0f / P.temperature;
+    if (invT != 1.0f) {
 #pragma unroll
-    for (int e = 0; e < NE; e++) v[e] *= invT;
-    if (!(invT > 0.0f)) {  // negative or NaN scale: pads go back to -inf
+        for (int e = 0; e < NE; e++) v[e] *= invT;
+        if (!(invT > 0.0f)) {  // negative or NaN scale: pads go back to -inf
 #pragma unroll
-        for (int e = 0; e < NE; e++)
-            if (eidx(e) >= V) v[e] = kNegInf;
+            for (int e = 0; e < NE; e++)
+                if (eidx(e) >= V) v[e] = kNegInf;
+        }
     }
     float mx, mn;  // max; min including -inf
     float fmn;     // min over finite entries
     uint32_t cnt;  // finite entries
     {
-        bool bad = false;
-        float tmx = kNegInf, tmn = kPosInf;
+        // the NaN-propagating maximum turns a NaN or +inf anywhere in a lane into a non-finite max
+        float tmx = v[0], tmn = v[0];
 #pragma unroll
-        for (int e = 0; e < NE; e++) {
-            bad |= __builtin_amdgcn_class(v[e], 0x203);  // NaN or +inf
-            tmx = fmaxf(tmx, v[e]);
+        for (int e = 1; e < NE; e++) {
+            tmx = __builtin_elementwise_maximum(tmx, v[e]);
             tmn = fminf(tmn, v[e]);
         }
-        if (__ballot(bad)) {
+        if (__ballot(!(tmx < kPosInf))) {
             if (lane == 0) a.out_ids[r] = VXS_ERR_NONFINITE;
             return 0;
         }
@@ -266,145 +271,186 @@ __device__ __forceinline__ int wave_fast_row(const SampleArgs& a, int vec, int r
     if (cnt <= (uint32_t)kExact) return 1;  // exact regime
 
     // ================= nucleus regime =================
-    const float m = mx;
     const double u = a.u ? a.u[r] : 0.0;
-    // F fraction bits: vocab * 2^F <= 2^53 (exact double sums) and e * 2^F < 2^52.
+    const double thr = (double)(1.0f - P.top_p);
+    const bool topp = P.top_p < 1.0f;
+    if (topp && !(thr < 1.0)) return 1;  // top_p <= 0: every entry but the last in order goes
+    // F fraction bits: vocab * 2^F <= 2^53, so sums of masses (multiples of 2^-F) are exact
     const int F = min(51, 53 - (32 - __clz(V - 1)));
-    const double scaleF = __builtin_ldexp(1.0, F);
+    const float Cb = mass_bias(F);
+    // 2^F and 2^-F built from their bits, so they stay in scalar registers
+    const double gF = __longlong_as_double((long long)(1023 + F) << 52);
+    const double gFi = __longlong_as_double((long long)(1023 - F) << 52);
+    // masses replace the logits: exp(x - max) in fp32 on the 2^-F grid; -inf entries get 0
 #pragma unroll
-    for (int e = 0; e < NE; e++) v[e] = v[e] - m;  // d = x - max; -inf stays -inf
-    // masses are recomputed from d where needed: the row and its masses together would not fit
-    auto qof = [&](int e) -> float { return exp_neg(opaque(v[e])); };
-    auto wof = [&](int e) -> double { return fixed_point((double)qof(e), scaleF); };
-    float dc = kNegInf;  // cut: keep d > dc, or d == dc with index >= ic
-    int ic = 0;
+    for (int e = 0; e < NE; e++) v[e] = mass_of(exp_neg(v[e] - mx), Cb);
+    float qc = 0.0f;  // cut: keep masses >= qc
     double Skept;
-    if (P.top_p < 1.0f) {
+    if (topp) {
         Sel& s = sm.u.sel;
-        for (int b = lane; b < kNB; b += 64) s.hist[b] = 0.0;
-        // buckets linear in d over [lo, 0]; masses below d = -32 round to zero
-        const float lo = fmaxf(fmn - m, -32.0f);
-        const float scale = lo < -1e-30f ? (float)kNB / -lo : 0.0f;
-        const float off = -lo * scale;
-        auto bucket = [&](float d) -> int {
-            return (int)__builtin_amdgcn_fmed3f(__builtin_fmaf(d, scale, off), 0.0f, (float)(kNB - 1));
-        };
-        wsync();
+        // Buckets: bits(mass) >> sh, a log scale, 1024 of them from `base` up. Every nonzero mass
+        // lies in [lb, bits(1) + 8]; zero masses land anywhere and add nothing. The physical
+        // bucket is the low 10 bits of the index, so no clamp is needed.
+        const float qmin = mass_of(exp_neg(fmn - mx), Cb);
+        const float qlow = qmin - qmin * 0x1p-18f - __uint_as_float((uint32_t)(127 - F) << 23);
+        const uint32_t lb = max(__float_as_uint(qlow), (uint32_t)(127 - F) << 23);
+        constexpr uint32_t kTop = 0x3f800000u + 8u;
+        int sh = max(3, (32 - __clz(kTop - lb)) - 10);
+        if ((kTop >> sh) + 2 - ((lb >> sh) & ~15u) > (uint32_t)kNB - 1) sh++;
+        const uint32_t base = (lb >> sh) & ~15u;
+        const uint32_t pbase = (base + (uint32_t)(kBPL * lane)) & (kNB - 1);
 #pragma unroll
-        for (int e = 0; e < NE; e++)  // -inf entries add 0
-            atomicAdd(&s.hist[bucket(v[e])], fixed_point((double)exp_neg(v[e]), scaleF));
+        for (int i = 0; i < kNB / 128; i++) *(dbl2*)&s.hist[(i * 64 + lane) * 2] = dbl2{0.0, 0.0};
         wsync();
-        // scan: lane l owns buckets [l*kBPL, (l+1)*kBPL)
-        double h[kBPL];
-        double lt = 0.0;
+        char* hb = (char*)s.hist;
 #pragma unroll
-        for (int j = 0; j < kBPL; j++) {
-            h[j] = s.hist[lane * kBPL + j];
-            lt += h[j];
+        for (int e = 0; e < NE; e++) {
+            const float q = opaque(v[e]);  // keeps the conversions next to their atomics
+            const uint32_t off = (__float_as_uint(q) >> (sh - 3)) & ((kNB - 1) << 3);
+            atomicAdd((double*)(hb + off), (double)q);
         }
+        wsync();
+        // lane totals in ascending bucket order, then the crossing lane, then the crossing bucket;
+        // lane l starts its 16 reads at bucket (l/2) mod 16 of its range, which spreads every read
+        // of the wave over all LDS banks
+        double lt = 0.0;
+        const int rot = lane >> 1;
+#pragma unroll
+        for (int j = 0; j < kBPL; j++) lt += s.hist[pbase + ((j + rot) & (kBPL - 1))];
         const double incl = wave_incl_sum(lt);
         const double S = readlane_d(incl, 63);
-        const double thr = (double)(1.0f - P.top_p);
-        if (!(thr < 1.0)) return 1;  // top_p <= 0: every entry but the last in order goes
-        const double T = floor(thr * S);
-        double run = incl - lt;
-        int mine = -1;
-        double mbelow = 0.0;
-#pragma unroll
-        for (int j = 0; j < kBPL; j++) {
-            const bool hit = run <= T && T - run < h[j];
-            mine = hit ? lane * kBPL + j : mine;
-            mbelow = hit ? run : mbelow;
-            run += h[j];
-        }
-        const uint64_t cb = __ballot(mine >= 0);
-        if (!cb) return 1;  // total <= T
-        const int pl = (int)__builtin_ctzll(cb);
-        const int bstar = (int)readlane((uint32_t)mine, pl);
-        const double below = readlane_d(mbelow, pl);
-        // gather the crossing bucket in index order (ballot compaction)
+        const double T = floor(thr * S * gF) * gFi;
+        const double run = incl - lt;
+        const uint64_t cb = __ballot(run <= T && T - run < lt);
+        if (!cb) return 1;
+        const int L = (int)__builtin_ctzll(cb);
+        const double runL = readlane_d(run, L);
+        const uint32_t pL = (base + (uint32_t)(kBPL * L)) & (kNB - 1);
+        const double hj = lane < kBPL ? s.hist[pL + (lane & (kBPL - 1))] : 0.0;
+        const double ij = row_incl_sum(hj);  // lanes 0..15 form one DPP row
+        const double xj = runL + (ij - hj);
+        const uint64_t jb = __ballot(lane < kBPL && xj <= T && T - xj < hj);
+        if (!jb) return 1;
+        const int jl = (int)__builtin_ctzll(jb);
+        const double below = readlane_d(xj, jl);
+        const uint32_t glo = (base + (uint32_t)(kBPL * L + jl)) << sh;  // bits of the bucket's masses
+        const uint32_t gw = 1u << sh;
+        // gather the crossing bucket (ballot compaction)
         uint32_t n = 0;
 #pragma unroll
         for (int e = 0; e < NE; e++) {
-            const float d = opaque(v[e]);
-            const bool p = d != kNegInf && bucket(d) == bstar;
+            const uint32_t qb = __float_as_uint(v[e]);
+            const bool p = qb - glo < gw;
             const uint64_t bal = __ballot(p);
             if (bal) {
                 const uint32_t pos = n + mbcnt(bal);
-                if (p && pos < (uint32_t)kL) {
-                    s.key[pos] = f2key(d);
-                    s.idx[pos] = eidx(e);
-                }
+                if (p && pos < (uint32_t)kL) s.key[pos] = ((uint64_t)qb << 32) | (uint32_t)eidx(e);
                 n += (uint32_t)__builtin_popcountll(bal);
             }
         }
         if (n > (uint32_t)kL) return 1;
+        if (lane < 4) s.key[n + lane] = ~0ull;
         wsync();
-        // rank by (key, index): lane l holds entry l and compares it with every entry
+        // rank by (mass, index): every lane compares its entry with all of them (broadcast reads)
         const int nn = (int)n;
-        const uint32_t ka = lane < nn ? s.key[lane] : 0xffffffffu;
-        const int ia = lane < nn ? s.idx[lane] : 0x7fffffff;
-        const double wa = lane < nn ? fixed_point((double)exp_neg(key2f(ka)), scaleF) : 0.0;
-        int rk = 0;
-        for (int b = 0; b < nn; b++) {
-            const uint32_t kb = readlane(ka, b);
-            const int ib = (int)readlane((uint32_t)ia, b);
-            rk += (kb < ka) || (kb == ka && ib < ia);
+        const uint64_t ka = lane < nn ? s.key[lane] : ~0ull;
+        uint32_t rk = 0;
+#pragma unroll 1
+        for (int b = 0; b < nn; b += 4) {
+            const uint64_t* kp = &s.key[b];
+            rk += (kp[0] < ka) + (kp[1] < ka) + (kp[2] < ka) + (kp[3] < ka);
         }
         if (lane < nn) {
-            s.ws[rk] = wa;
-            s.at[rk] = lane;
+            s.ws[rk] = (double)__uint_as_float((uint32_t)(ka >> 32));
+            s.skey[rk] = ka;
         }
         wsync();
         const double w0 = lane < nn ? s.ws[lane] : 0.0;
-        const double c0 = below + wave_incl_sum(w0) - w0;
-        const uint64_t rb = __ballot(lane < nn && T >= c0 && T - c0 < w0);
+        const double c0 = below + (wave_incl_sum(w0) - w0);
+        const uint64_t rb = __ballot(lane < nn && c0 <= T && T - c0 < w0);
         if (!rb) return 1;
         const int rl = (int)__builtin_ctzll(rb);
-        const int at = s.at[rl];
-        dc = key2f(s.key[at]);
-        ic = s.idx[at];
+        const uint32_t kc = (uint32_t)(s.skey[rl] >> 32);
+        qc = __uint_as_float(kc);
+        // The masses are a monotone function of the logit (exp_neg is monotone on gfx950 —
+        // checked over every float in [-128, 0] — and the rounding to the 2^-F grid is
+        // monotone), so (mass, index) order is (logit, index) order except inside a group of
+        // equal masses. A cut inside such a group keeps its higher indices, which is the
+        // reference's choice when the group's logits are equal; they are wherever the cut's mass
+        // lies in [2^-16, 2^-6] (logits 4 to 11 below the max, where distinct logits never share a
+        // mass). A cut inside a group elsewhere sends the row to the general path.
+        if (rl > 0 && (uint32_t)(s.skey[rl - 1] >> 32) == kc) {
+            if (!(qc >= 0x1p-16f && qc <= 0x1p-6f)) return 1;
+            // the group's entries below the cut index are removed: their masses become 0
+            const int ic = (int)(uint32_t)s.skey[rl];
+#pragma unroll
+            for (int e = 0; e < NE; e++)
+                if (v[e] == qc && eidx(e) < ic) v[e] = 0.0f;
+        }
         Skept = S - readlane_d(c0, rl);
     } else {
         double ls = 0.0;
 #pragma unroll
-        for (int e = 0; e < NE; e++) ls += wof(e);
+        for (int e = 0; e < NE; e++) ls += (double)opaque(v[e]);
         Skept = wave_sum(ls);
     }
-    auto kept = [&](int e) { return v[e] > dc || (v[e] == dc && eidx(e) >= ic); };
 
-    // ---- draw: first kept index (index order) whose inclusive prefix mass exceeds floor(u * Skept)
-    const double D = floor(u * Skept);
-    int pick = -1;
-    double run = 0.0;
+    // ---- draw: first index (index order) whose inclusive kept-mass prefix exceeds floor(u * Skept)
+    const double D = floor(u * Skept * gF) * gFi;
+    int pick;
+    {
+        // per-lane kept mass of each sweep, [lane][NS], over the histogram (whose last reads
+        // precede the ranking's wave syncs), stored two sweeps at a time to keep few doubles live
+        double* pp = sm.u.sel.hist;
 #pragma unroll
-    for (int c = 0; c < NS; c++) {
-        if (pick < 0) {
-            double w4[4];
-            double mine = 0.0;
+        for (int c = 0; c < NS; c += 2) {
+            double ps[2] = {0.0, 0.0};
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                w4[j] = kept(c * 4 + j) ? wof(c * 4 + j) : 0.0;
-                mine += w4[j];
+            for (int k = 0; k < 8; k++) {
+                const float q = v[c * 4 + k];
+                ps[k >> 2] += (double)(q >= qc ? q : 0.0f);
             }
-            const double incl = wave_incl_sum(mine);
-            const double tot = readlane_d(incl, 63);
-            if (D < run + tot) {
-                double acc = run + incl - mine;
-                int hit = -1;
+            *(dbl2*)&pp[lane * NS + c] = dbl2{ps[0], ps[1]};
+        }
+        wsync();
+        // sweep totals: lanes 4c..4c+3 each add 16 lanes' sums of sweep c, then combine in the quad
+        const int sc = lane >> 2;
+        double t = 0.0;
+        if (sc < NS) {
+            const int part = lane & 3;
+            const double* col = pp + part * 16 * NS + sc;
+#pragma unroll
+            for (int i = 0; i < 16; i++) t += col[((i + 4 * part) & 15) * NS];  // rotated: fewer bank conflicts
+        }
+        t = quad_sum(t);
+        const double x = (lane & 3) == 0 ? t : 0.0;  // lanes past 4*NS hold 0
+        const double xi = wave_incl_sum(x);
+        const uint64_t sb = __ballot((lane & 3) == 0 && sc < NS && D < xi);
+        if (!sb) return 1;  // no crossing (rounding at the top of the range): general path
+        const int sl = (int)__builtin_ctzll(sb);
+        const int cs = sl >> 2;
+        const double before = readlane_d(xi, sl) - readlane_d(x, sl);
+        const double mine = pp[lane * NS + cs];
+        const double li = before + wave_incl_sum(mine);
+        const uint64_t lb2 = __ballot(D < li);
+        if (!lb2) return 1;
+        const int L2 = (int)__builtin_ctzll(lb2);
+        pick = -1;
+#pragma unroll
+        for (int c = 0; c < NS; c++) {
+            if (c == cs) {
+                double acc = li - mine;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    acc += w4[j];
-                    hit = (hit < 0 && w4[j] > 0.0 && D < acc) ? eidx(c * 4 + j) : hit;
+                    const float q = opaque(v[c * 4 + j]);  // recomputed, not kept from the sums
+                    acc += (double)(q >= qc ? q : 0.0f);
+                    pick = (pick < 0 && D < acc) ? eidx(c * 4 + j) : pick;
                 }
-                const uint64_t bal = __ballot(hit >= 0);
-                pick = (int)readlane((uint32_t)hit, bal ? (int)__builtin_ctzll(bal) : 0);
-            } else {
-                run += tot;
             }
         }
+        pick = (int)readlane((uint32_t)pick, L2);
     }
-    if (pick < 0) return 1;  // no crossing (rounding at the top of the range): general path
+    if (pick < 0) return 1;
     if (lane == 0) a.out_ids[r] = pick;
     return 0;
 }

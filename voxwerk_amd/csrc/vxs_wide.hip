@@ -670,7 +670,8 @@ __global__ __launch_bounds__(kTW) void sample_wide_kernel(SampleArgs a, int vec)
     // fixed-point masses of d = x - max
     const int F = min(51, 53 - (32 - __clz(V - 1)));
     const double scaleF = __builtin_ldexp(1.0, F);
-    auto wof = [&](float v) -> double { return fixed_point((double)exp_neg(v - mx), scaleF); };
+    const float Cb = mass_bias(F);
+    auto wof = [&](float v) -> double { return fixed_mass(exp_neg(v - mx), Cb, scaleF); };
     float dc = kNegInf;  // cut: keep d > dc, or d == dc with index >= ic
     int ic = 0;
     double Skept;
