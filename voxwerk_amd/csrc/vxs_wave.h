@@ -43,6 +43,7 @@ constexpr int kSweep = 256;  // elements per sweep: 64 lanes x 4
 constexpr int kPart = 6;     // sweeps staged in LDS at once for the penalty
 constexpr int kNB = 1024;    // top-p histogram buckets (16 per lane)
 constexpr int kBPL = kNB / 64;
+static_assert(kNB == 1024, "bucket index is a 10-bit field of the mass bits");
 constexpr int kL = 64;       // crossing-bucket entries ranked exactly (one per lane)
 constexpr int kExact = 256;  // rows with at most this many candidates take the exact regime
 constexpr int kHP = 8;       // history ids per lane fetched with the row (512 per row)
@@ -82,72 +83,106 @@ __device__ __forceinline__ uint32_t mbcnt(uint64_t bal) {
 template <int NS>
 struct WaveSmem {
     union {
-        float xs[wave::kPart * wave::kSweep];  // penalty staging
+        float xs[wave::kPart * wave::kSweep + 64];  // penalty staging, then one spare slot per lane
         wave::Sel sel;
     } u;
 };
 
-// Samples row r with one wave. Returns 0 when the row is done (its id written) and 1, having
-// written nothing, when it must go to the general algorithm.
 template <int NS>
-__device__ __forceinline__ int wave_fast_row(const SampleArgs& a, int vec, int r, int lane, WaveSmem<NS>& sm) {
+struct WaveRow {
+    float v[4 * NS];     // the row: lane l holds elements c*256 + 4l + j
+    int pre[wave::kHP];  // history ids h0 + lane + 64k
+    int h0, h1;          // the row's history range
+    bool pen_on;         // penalty active
+};
+
+// The loads of row r (in the batch), issued without waiting.
+template <int NS>
+__device__ __forceinline__ void wave_load_row(const SampleArgs& a, int vec, int r, int lane, WaveRow<NS>& w) {
     using namespace wave;
-    constexpr int NE = 4 * NS;
     const int V = a.vocab;
-    if (a.out_logits || a.out_probs || (a.kflags & KF_STOP_AFTER_PENALTY)) return 1;
-    const vxs_params P = a.params[(int64_t)r * a.params_stride];
-    if (P.do_sample && P.top_k > 0 && P.top_k < V) return 1;
-
     const float* __restrict__ xrow = a.logits + (int64_t)r * a.ld;
-    const bool pen_on = P.rep_penalty != 1.0f && a.hist_off != nullptr;
-    if (pen_on && a.hist_off[r + 1] - a.hist_off[r] > kHP * 64) return 1;  // long history
-    // element index of register slot e; the base is re-materialised at each use so the compiler
-    // does not keep an index register per element alive
     const int lane4 = lane * 4;
-    auto eidx = [&](int e) { return (e >> 2) * kSweep + opaque_i(lane4) + (e & 3); };
-
-    // ---- issue the history prefetch and the row loads together
-    int h0 = 0, h1 = 0;
-    int pre[kHP];
-    if (pen_on) {
-        h0 = a.hist_off[r];
-        h1 = a.hist_off[r + 1];
-#pragma unroll
-        for (int k = 0; k < kHP; k++) {
-            const int h = h0 + lane + k * 64;
-            pre[k] = h < h1 ? a.hist_ids[h] : 0;
-        }
-    }
-    float v[NE];
 #pragma unroll
     for (int c = 0; c < NS; c++) {
         if (vec && (c + 1) * kSweep <= V) {  // whole sweep inside the row (wave-uniform)
             typedef float f4 __attribute__((ext_vector_type(4)));
             const f4 q = __builtin_nontemporal_load((const f4*)(xrow + c * kSweep + lane4));
-            v[c * 4 + 0] = q.x;
-            v[c * 4 + 1] = q.y;
-            v[c * 4 + 2] = q.z;
-            v[c * 4 + 3] = q.w;
+            w.v[c * 4 + 0] = q.x;
+            w.v[c * 4 + 1] = q.y;
+            w.v[c * 4 + 2] = q.z;
+            w.v[c * 4 + 3] = q.w;
         } else {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int i = c * kSweep + lane4 + j;
-                v[c * 4 + j] = i < V ? xrow[i] : kNegInf;
+                w.v[c * 4 + j] = i < V ? xrow[i] : kNegInf;
             }
         }
     }
+}
+
+// The checks that hand a row back to the general algorithm, then the loads of its history, issued
+// without waiting. Returns 1 to hand the row back, else 0.
+template <int NS>
+__device__ __forceinline__ int wave_prepare(const SampleArgs& a, int r, int lane, const vxs_params& P, WaveRow<NS>& w) {
+    using namespace wave;
+    if (a.out_logits || a.out_probs || (a.kflags & KF_STOP_AFTER_PENALTY)) return 1;
+    if (P.do_sample && P.top_k > 0 && P.top_k < a.vocab) return 1;
+    w.pen_on = P.rep_penalty != 1.0f && a.hist_off != nullptr;
+    w.h0 = w.h1 = 0;
+    if (w.pen_on) {
+        w.h0 = a.hist_off[r];
+        w.h1 = a.hist_off[r + 1];
+        if (w.h1 - w.h0 > kHP * 64) return 1;  // long history
+#pragma unroll
+        for (int k = 0; k < kHP; k++) {
+            const int h = w.h0 + lane + k * 64;
+            w.pre[k] = h < w.h1 ? a.hist_ids[h] : 0;
+        }
+    }
+    return 0;
+}
+
+// Second half: samples row r from its loaded logits. Returns 0 when the row is done (its id
+// written) and 1, having written nothing, when it must go to the general algorithm.
+template <int NS>
+__device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane, const vxs_params& P, WaveRow<NS>& w,
+                                           WaveSmem<NS>& sm) {
+    using namespace wave;
+    constexpr int NE = 4 * NS;
+    const int V = a.vocab;
+    // element index of register slot e; the base is re-materialised at each use so the compiler
+    // does not keep an index register per element alive
+    const int lane4 = lane * 4;
+    auto eidx = [&](int e) { return (e >> 2) * kSweep + opaque_i(lane4) + (e & 3); };
+    float (&v)[NE] = w.v;
+    const int(&pre)[kHP] = w.pre;
+    const int h0 = w.h0, h1 = w.h1;
+    const bool pen_on = w.pen_on;
     // entries past the vocabulary (pads) hold -inf: they never win, carry no mass, are never written
 
     // ---- S1: repetition penalty over the distinct history ids
     // Per staged part, every lane first reads the original logit of each of its ids, then writes
     // the penalised value back: a wave's LDS operations execute in order, so all reads precede all
-    // writes and a repeated id writes the same value again instead of being penalised twice.
+    // writes and a repeated id writes the same value again instead of being penalised twice. The
+    // reads and writes are unmasked: an id outside the part uses the lane's own spare slot.
     if (pen_on && h1 > h0) {
         const float rho = P.rep_penalty;
         const float rinv = 1.0f / rho;
         const float arho = __builtin_fabsf(rho);
         const bool fast = arho >= 0x1p-60f && arho <= 0x1p60f;
+        bool live[kHP];
         bool bad = false;
+#pragma unroll
+        for (int k = 0; k < kHP; k++) {
+            live[k] = h0 + lane + k * 64 < h1;
+            bad |= live[k] && (unsigned)pre[k] >= (unsigned)V;
+        }
+        if (__ballot(bad)) {
+            if (lane == 0) a.out_ids[r] = VXS_ERR_ID_OUT_OF_RANGE;
+            return 0;
+        }
         float* xs = sm.u.xs;
         typedef float f4 __attribute__((ext_vector_type(4)));
 #pragma unroll
@@ -158,22 +193,28 @@ __device__ __forceinline__ int wave_fast_row(const SampleArgs& a, int vec, int r
                     *(f4*)(xs + c * kSweep + lane4) =
                         f4{v[(p0 + c) * 4 + 0], v[(p0 + c) * 4 + 1], v[(p0 + c) * 4 + 2], v[(p0 + c) * 4 + 3]};
             wsync();
-            const int lo = p0 * kSweep, hi = (p0 + kPart < NS ? p0 + kPart : NS) * kSweep;
+            const int lo = p0 * kSweep, span = (p0 + kPart < NS ? kPart : NS - p0) * kSweep;
             {
-                float sv[kHP];
+                int at[kHP];
+                float pv[kHP];
+                bool slow = false;
 #pragma unroll
                 for (int k = 0; k < kHP; k++) {
-                    const int id = pre[k];
-                    const bool in = h0 + lane + k * 64 < h1 && id >= lo && id < hi;
-                    sv[k] = in ? xs[id - lo] : 0.0f;
+                    const bool in = live[k] && (unsigned)(pre[k] - lo) < (unsigned)span;
+                    at[k] = in ? pre[k] - lo : kPart * kSweep + lane;
+                    const float sv = xs[at[k]];
+                    pv[k] = penalize_fast(sv, rho, rinv);
+                    slow |= in && penalize_needs_division(sv, fast);
+                }
+                if (__ballot(slow)) {  // zeros, non-finite or extreme values: IEEE division
+#pragma unroll
+                    for (int k = 0; k < kHP; k++) {
+                        const float sv = xs[at[k]];
+                        if (penalize_needs_division(sv, fast)) pv[k] = sv / rho;
+                    }
                 }
 #pragma unroll
-                for (int k = 0; k < kHP; k++) {
-                    const int id = pre[k];
-                    const bool live = h0 + lane + k * 64 < h1;
-                    bad |= live && (unsigned)id >= (unsigned)V;
-                    if (live && id >= lo && id < hi) xs[id - lo] = penalize(sv[k], rho, rinv, fast);
-                }
+                for (int k = 0; k < kHP; k++) xs[at[k]] = pv[k];
             }
             wsync();
 #pragma unroll
@@ -186,10 +227,6 @@ __device__ __forceinline__ int wave_fast_row(const SampleArgs& a, int vec, int r
                     v[(p0 + c) * 4 + 3] = q.w;
                 }
             wsync();  // the next part (or phase) overwrites the staging area
-        }
-        if (__ballot(bad)) {
-            if (lane == 0) a.out_ids[r] = VXS_ERR_ID_OUT_OF_RANGE;
-            return 0;
         }
     }
 
@@ -295,20 +332,16 @@ __device__ __forceinline__ int wave_fast_row(const SampleArgs& a, int vec, int r
         const float qlow = qmin - qmin * 0x1p-18f - __uint_as_float((uint32_t)(127 - F) << 23);
         const uint32_t lb = max(__float_as_uint(qlow), (uint32_t)(127 - F) << 23);
         constexpr uint32_t kTop = 0x3f800000u + 8u;
-        int sh = max(3, (32 - __clz(kTop - lb)) - 10);
+        int sh = max(0, (32 - __clz(kTop - lb)) - 10);
         if ((kTop >> sh) + 2 - ((lb >> sh) & ~15u) > (uint32_t)kNB - 1) sh++;
         const uint32_t base = (lb >> sh) & ~15u;
         const uint32_t pbase = (base + (uint32_t)(kBPL * lane)) & (kNB - 1);
 #pragma unroll
         for (int i = 0; i < kNB / 128; i++) *(dbl2*)&s.hist[(i * 64 + lane) * 2] = dbl2{0.0, 0.0};
         wsync();
-        char* hb = (char*)s.hist;
 #pragma unroll
-        for (int e = 0; e < NE; e++) {
-            const float q = opaque(v[e]);  // keeps the conversions next to their atomics
-            const uint32_t off = (__float_as_uint(q) >> (sh - 3)) & ((kNB - 1) << 3);
-            atomicAdd((double*)(hb + off), (double)q);
-        }
+        for (int e = 0; e < NE; e++)
+            atomicAdd(&s.hist[__builtin_amdgcn_ubfe(__float_as_uint(v[e]), (uint32_t)sh, 10u)], (double)v[e]);
         wsync();
         // lane totals in ascending bucket order, then the crossing lane, then the crossing bucket;
         // lane l starts its 16 reads at bucket (l/2) mod 16 of its range, which spreads every read
@@ -391,7 +424,7 @@ __device__ __forceinline__ int wave_fast_row(const SampleArgs& a, int vec, int r
     } else {
         double ls = 0.0;
 #pragma unroll
-        for (int e = 0; e < NE; e++) ls += (double)opaque(v[e]);
+        for (int e = 0; e < NE; e++) ls += (double)opaque(v[e]);  // opaque: no conversion shared with the histogram
         Skept = wave_sum(ls);
     }
 
@@ -453,6 +486,16 @@ __device__ __forceinline__ int wave_fast_row(const SampleArgs& a, int vec, int r
     if (pick < 0) return 1;
     if (lane == 0) a.out_ids[r] = pick;
     return 0;
+}
+
+// Samples row r (r < a.rows) with one wave: 0 when done, 1 when handed back.
+template <int NS>
+__device__ __forceinline__ int wave_fast_row(const SampleArgs& a, int vec, int r, int lane, WaveSmem<NS>& sm) {
+    WaveRow<NS> w;
+    const vxs_params P = a.params[(int64_t)r * a.params_stride];
+    if (wave_prepare<NS>(a, r, lane, P, w)) return 1;
+    wave_load_row<NS>(a, vec, r, lane, w);  // after the history loads: measured faster than before them
+    return wave_finish<NS>(a, r, lane, P, w, sm);
 }
 
 }  // namespace vxs
