@@ -51,7 +51,7 @@ constexpr int kHP = 8;       // history ids per lane fetched with the row (512 p
 typedef double dbl2 __attribute__((ext_vector_type(2)));
 
 struct Sel {
-    alignas(16) double hist[kNB];       // mass per bucket; then the draw's per-lane sweep sums
+    alignas(16) uint64_t hist[kNB];     // mass per bucket in units of 2^-F; then the draw's per-lane sweep sums
     uint64_t key[kL + 4];   // crossing-bucket entries: mass bits << 32 | index, then 4 pads
     uint64_t skey[kL];      // the same in rank order
     double ws[kL];          // their masses in rank order
@@ -337,19 +337,28 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         const uint32_t base = (lb >> sh) & ~15u;
         const uint32_t pbase = (base + (uint32_t)(kBPL * lane)) & (kNB - 1);
 #pragma unroll
-        for (int i = 0; i < kNB / 128; i++) *(dbl2*)&s.hist[(i * 64 + lane) * 2] = dbl2{0.0, 0.0};
+        for (int i = 0; i < kNB / 128; i++) *(dbl2*)&s.hist[(i * 64 + lane) * 2] = dbl2{0.0, 0.0};  // zero bits
         wsync();
+        // Integer atomics (LDS adds u64 faster than f64): a mass below 2^(52-F) added to 2^(52-F) in
+        // double precision leaves mass * 2^F, an integer below 2^52, in the mantissa bits (the sum
+        // keeps the exponent of 2^(52-F), so the high word just loses its exponent bits).
+        const double big = __longlong_as_double((long long)(1023 + 52 - F) << 52);
 #pragma unroll
-        for (int e = 0; e < NE; e++)
-            atomicAdd(&s.hist[__builtin_amdgcn_ubfe(__float_as_uint(v[e]), (uint32_t)sh, 10u)], (double)v[e]);
+        for (int e = 0; e < NE; e++) {
+            const uint64_t tb = (uint64_t)__double_as_longlong((double)v[e] + big);
+            const uint64_t iq = (tb & 0xffffffffull) | ((uint64_t)((uint32_t)(tb >> 32) & 0xfffffu) << 32);
+            atomicAdd((unsigned long long*)&s.hist[__builtin_amdgcn_ubfe(__float_as_uint(v[e]), (uint32_t)sh, 10u)],
+                      (unsigned long long)iq);
+        }
         wsync();
         // lane totals in ascending bucket order, then the crossing lane, then the crossing bucket;
         // lane l starts its 16 reads at bucket (l/2) mod 16 of its range, which spreads every read
         // of the wave over all LDS banks
-        double lt = 0.0;
+        uint64_t lti = 0;
         const int rot = lane >> 1;
 #pragma unroll
-        for (int j = 0; j < kBPL; j++) lt += s.hist[pbase + ((j + rot) & (kBPL - 1))];
+        for (int j = 0; j < kBPL; j++) lti += s.hist[pbase + ((j + rot) & (kBPL - 1))];
+        const double lt = (double)lti * gFi;  // exact: below 2^53 units of 2^-F
         const double incl = wave_incl_sum(lt);
         const double S = readlane_d(incl, 63);
         const double T = floor(thr * S * gF) * gFi;
@@ -359,7 +368,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         const int L = (int)__builtin_ctzll(cb);
         const double runL = readlane_d(run, L);
         const uint32_t pL = (base + (uint32_t)(kBPL * L)) & (kNB - 1);
-        const double hj = lane < kBPL ? s.hist[pL + (lane & (kBPL - 1))] : 0.0;
+        const double hj = lane < kBPL ? (double)s.hist[pL + (lane & (kBPL - 1))] * gFi : 0.0;
         const double ij = row_incl_sum(hj);  // lanes 0..15 form one DPP row
         const double xj = runL + (ij - hj);
         const uint64_t jb = __ballot(lane < kBPL && xj <= T && T - xj < hj);
@@ -434,7 +443,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
     {
         // per-lane kept mass of each sweep, [lane][NS], over the histogram (whose last reads
         // precede the ranking's wave syncs), stored two sweeps at a time to keep few doubles live
-        double* pp = sm.u.sel.hist;
+        double* pp = reinterpret_cast<double*>(sm.u.sel.hist);
 #pragma unroll
         for (int c = 0; c < NS; c += 2) {
             double ps[2] = {0.0, 0.0};
