@@ -36,6 +36,15 @@ __device__ __forceinline__ uint64_t dpp64(uint64_t old, uint64_t x) {
     return ((uint64_t)hi << 32) | lo;
 }
 
+// The same for a full row and bank mask with bound_ctrl: lanes whose source is outside the row read
+// 0, and no `old` value needs to be set up.
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp64z(uint64_t x) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)x, CTRL, 0xf, 0xf, true);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(x >> 32), CTRL, 0xf, 0xf, true);
+    return ((uint64_t)hi << 32) | lo;
+}
+
 __device__ __forceinline__ uint32_t readlane(uint32_t x, int lane) {
     return (uint32_t)__builtin_amdgcn_readlane((int)x, lane);
 }
@@ -66,20 +75,22 @@ __device__ __forceinline__ uint32_t wave_sum(uint32_t x) { return readlane(wave_
 __device__ __forceinline__ uint64_t wave_sum(uint64_t x) { return readlane64(wave_incl_sum(x), 63); }
 
 __device__ __forceinline__ double wave_incl_sum(double x) {
+#define VXS_FSTEPZ(C) x += __longlong_as_double((long long)dpp64z<C>((uint64_t)__double_as_longlong(x)));
 #define VXS_FSTEP(C, M) \
     x += __longlong_as_double((long long)dpp64<C, M>(0, (uint64_t)__double_as_longlong(x)));
-    VXS_FSTEP(kRowShr1, 0xf)
-    VXS_FSTEP(kRowShr2, 0xf)
-    VXS_FSTEP(kRowShr4, 0xf)
-    VXS_FSTEP(kRowShr8, 0xf)
+    VXS_FSTEPZ(kRowShr1)
+    VXS_FSTEPZ(kRowShr2)
+    VXS_FSTEPZ(kRowShr4)
+    VXS_FSTEPZ(kRowShr8)
     VXS_FSTEP(kRowBcast15, 0xa)
     VXS_FSTEP(kRowBcast31, 0xc)
 #undef VXS_FSTEP
+#undef VXS_FSTEPZ
     return x;
 }
 // Inclusive prefix sum inside each row of 16 lanes.
 __device__ __forceinline__ double row_incl_sum(double x) {
-#define VXS_FSTEP(C) x += __longlong_as_double((long long)dpp64<C>(0, (uint64_t)__double_as_longlong(x)));
+#define VXS_FSTEP(C) x += __longlong_as_double((long long)dpp64z<C>((uint64_t)__double_as_longlong(x)));
     VXS_FSTEP(kRowShr1)
     VXS_FSTEP(kRowShr2)
     VXS_FSTEP(kRowShr4)
@@ -89,8 +100,8 @@ __device__ __forceinline__ double row_incl_sum(double x) {
 }
 // Sum over each quad of lanes, in every lane of the quad.
 __device__ __forceinline__ double quad_sum(double x) {
-    x += __longlong_as_double((long long)dpp64<kQuadSwap1>(0, (uint64_t)__double_as_longlong(x)));
-    x += __longlong_as_double((long long)dpp64<kQuadSwap2>(0, (uint64_t)__double_as_longlong(x)));
+    x += __longlong_as_double((long long)dpp64z<kQuadSwap1>((uint64_t)__double_as_longlong(x)));
+    x += __longlong_as_double((long long)dpp64z<kQuadSwap2>((uint64_t)__double_as_longlong(x)));
     return x;
 }
 __device__ __forceinline__ double readlane_d(double x, int lane) {
@@ -243,8 +254,10 @@ __device__ __forceinline__ bool penalize_needs_division(float s, bool fast) {
 // exp(d) for d <= 0 in fp32: 2^(d log2 e) with the product carried in two parts (the rounding
 // error of d*L2E recovered by fma, plus d times the tail of log2 e) and the hardware 2^x. Relative
 // error about 1e-7; 0 for d = -inf or results below 2^-126 (d is clamped at -256 first).
-__device__ __forceinline__ float exp_neg(float d) {
-    d = __builtin_fmaxf(d, -256.0f);
+__device__ __forceinline__ float exp_neg_unclamped(float d);
+__device__ __forceinline__ float exp_neg(float d) { return exp_neg_unclamped(__builtin_fmaxf(d, -256.0f)); }
+// The same without the clamp, for d in [-256, 0] (where the clamp changes nothing).
+__device__ __forceinline__ float exp_neg_unclamped(float d) {
     constexpr float kL2E = 1.44269502162933349609375f;          // fl32(log2 e)
     constexpr float kL2ELo = 1.925963033500011079e-8f;          // log2 e - kL2E
     constexpr float kLn2 = 0.693147180559945309f;

@@ -319,8 +319,13 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
     const double gF = __longlong_as_double((long long)(1023 + F) << 52);
     const double gFi = __longlong_as_double((long long)(1023 - F) << 52);
     // masses replace the logits: exp(x - max) in fp32 on the 2^-F grid; -inf entries get 0
+    if (mn != kNegInf && fmn - mx >= -256.0f) {  // every d in [-256, 0]: exp_neg's clamp is the identity
 #pragma unroll
-    for (int e = 0; e < NE; e++) v[e] = mass_of(exp_neg(v[e] - mx), Cb);
+        for (int e = 0; e < NE; e++) v[e] = mass_of(exp_neg_unclamped(v[e] - mx), Cb);
+    } else {
+#pragma unroll
+        for (int e = 0; e < NE; e++) v[e] = mass_of(exp_neg(v[e] - mx), Cb);
+    }
     float qc = 0.0f;  // cut: keep masses >= qc
     double Skept;
     if (topp) {
@@ -352,12 +357,12 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         }
         wsync();
         // lane totals in ascending bucket order, then the crossing lane, then the crossing bucket;
-        // lane l starts its 16 reads at bucket (l/2) mod 16 of its range, which spreads every read
-        // of the wave over all LDS banks
+        // lane l reads its 16 buckets in the order j xor (l/2 mod 16), which spreads every read of
+        // the wave over all LDS banks
         uint64_t lti = 0;
-        const int rot = lane >> 1;
+        const int rot = (lane >> 1) & (kBPL - 1);
 #pragma unroll
-        for (int j = 0; j < kBPL; j++) lti += s.hist[pbase + ((j + rot) & (kBPL - 1))];
+        for (int j = 0; j < kBPL; j++) lti += s.hist[pbase + (j ^ rot)];
         const double lt = (double)lti * gFi;  // exact: below 2^53 units of 2^-F
         const double incl = wave_incl_sum(lt);
         const double S = readlane_d(incl, 63);
@@ -379,10 +384,12 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         const uint32_t gw = 1u << sh;
         // gather the crossing bucket (ballot compaction)
         uint32_t n = 0;
+        uint32_t gwo = gw;
+        asm volatile("" : "+s"(gwo));  // a plain unsigned compare (not rewritten into a shift and a test)
 #pragma unroll
         for (int e = 0; e < NE; e++) {
             const uint32_t qb = __float_as_uint(v[e]);
-            const bool p = qb - glo < gw;
+            const bool p = qb - glo < gwo;
             const uint64_t bal = __ballot(p);
             if (bal) {
                 const uint32_t pos = n + mbcnt(bal);
