@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstring>
 #include <new>
@@ -13,6 +14,8 @@
 namespace {
 
 constexpr size_t kAlign = 256;
+constexpr int kPolledMaxRows = 1024;                        // host calls below this complete by polling
+constexpr std::chrono::seconds kPollLimit{2};              // then a stream synchronisation takes over
 size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
 
 // Device buffer that only grows.
@@ -44,6 +47,7 @@ struct DevBuf {
 struct HostBuf {
     void* p = nullptr;
     size_t cap = 0;
+    unsigned flags = hipHostMallocDefault;
     hipError_t reserve(size_t n) {
         if (n <= cap) return hipSuccess;
         if (p) {
@@ -53,7 +57,7 @@ struct HostBuf {
             if (e != hipSuccess) return e;
         }
         size_t want = std::max(n, cap + cap / 2);
-        hipError_t e = hipHostMalloc(&p, want, hipHostMallocDefault);
+        hipError_t e = hipHostMalloc(&p, want, flags);
         if (e != hipSuccess) return e;
         cap = want;
         return hipSuccess;
@@ -77,6 +81,12 @@ struct vxs_ctx {
     size_t defer_rows = 0;
     int defer_phase = 0;  // which counter the next call uses
     HostBuf h_in, h_ids, h_out;
+    // completion by polling (small host calls on the one-workgroup-per-row path): a device counter,
+    // zeroed once, and coherent pinned memory holding the flag (word 0) and the ids (from word 16)
+    DevBuf d_done;
+    bool done_ready = false;
+    HostBuf h_done;
+    int32_t done_seq = 0;
 };
 
 namespace {
@@ -223,7 +233,8 @@ int check_flags(vxs_ctx* ctx, uint32_t flags) {
 // Stage inputs and launch. On success the kernel is queued on ctx->stream.
 int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int64_t ld, const int32_t* hist_off,
                      const int32_t* hist_ids, const vxs_params* params, int params_stride, const double* u,
-                     bool want_logits, bool want_probs, uint32_t kflags, uint32_t flags = 0) {
+                     bool want_logits, bool want_probs, uint32_t kflags, uint32_t flags = 0,
+                     const vxs::SampleArgs* done = nullptr) {
     const Layout L = plan(rows, vocab, params_stride, hist_off);
     VXS_HIP(ctx, ctx->h_in.reserve(L.total));
     VXS_HIP(ctx, ctx->d_in.reserve(L.total));
@@ -264,8 +275,62 @@ int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int
     a.out_probs = want_probs ? static_cast<double*>(ctx->d_probs_out.p) : nullptr;
     a.kflags = kflags;
     a.path = choose_path(flags, rows, vocab);
+    if (done) {
+        a.out_ids = done->out_ids;
+        a.done_count = done->done_count;
+        a.done_flag = done->done_flag;
+        a.done_seq = done->done_seq;
+    }
     if (a.path == vxs::kPathQuad) VXS_HIP(ctx, ensure_defer(ctx, rows, a));
     VXS_HIP(ctx, launch_checked(ctx, a));
+    return VXS_OK;
+}
+
+// Host calls that can complete by polling: the one-workgroup-per-row kernel alone, ids only.
+bool polled_call(int rows, int vocab, uint32_t flags, bool want_logits, bool want_probs) {
+    return !want_logits && !want_probs && vocab <= vxs::kRowResidentMaxVocab &&
+           choose_path(flags, rows, vocab) == vxs::kPathBlock && rows <= kPolledMaxRows;
+}
+
+// Completion state for a polled call of `rows` rows: the device counter (zeroed when first used and
+// after any failure) and the coherent host words the kernel writes.
+hipError_t ensure_done(vxs_ctx* ctx, int rows, vxs::SampleArgs& a) {
+    if (!ctx->done_ready) {
+        hipError_t e = ctx->d_done.reserve(sizeof(int32_t));
+        if (e != hipSuccess) return e;
+        if ((e = hipMemset(ctx->d_done.p, 0, sizeof(int32_t))) != hipSuccess) return e;
+        ctx->done_ready = true;
+    }
+    ctx->h_done.flags = hipHostMallocCoherent;
+    hipError_t e = ctx->h_done.reserve(sizeof(int32_t) * (16 + (size_t)rows));
+    if (e != hipSuccess) return e;
+    int32_t* w = static_cast<int32_t*>(ctx->h_done.p);
+    a.done_count = static_cast<int32_t*>(ctx->d_done.p);
+    a.done_flag = w;
+    a.done_seq = ++ctx->done_seq;
+    a.out_ids = w + 16;
+    return hipSuccess;
+}
+
+// Spin until the kernel publishes `seq`; after kPollLimit fall back to a stream synchronisation,
+// which reports a failed kernel.
+int wait_done(vxs_ctx* ctx, int32_t seq) {
+    const int32_t* flag = static_cast<const int32_t*>(ctx->h_done.p);
+    const auto t0 = std::chrono::steady_clock::now();
+    while (__atomic_load_n(flag, __ATOMIC_ACQUIRE) != seq) {
+        if (std::chrono::steady_clock::now() - t0 > kPollLimit) {
+            const hipError_t e = hipStreamSynchronize(ctx->stream);
+            if (e != hipSuccess) {
+                ctx->done_ready = false;
+                return hip_fail(ctx, e, "hipStreamSynchronize");
+            }
+            if (__atomic_load_n(flag, __ATOMIC_ACQUIRE) != seq) {
+                ctx->done_ready = false;
+                return fail(ctx, VXS_ERR_HIP, "kernel finished without publishing its completion");
+            }
+            break;
+        }
+    }
     return VXS_OK;
 }
 
@@ -326,6 +391,8 @@ VXS_API void vxs_destroy(vxs_ctx* ctx) {
     ctx->d_in.release();
     ctx->d_ids.release();
     ctx->d_defer.release();
+    ctx->d_done.release();
+    ctx->h_done.release();
     ctx->d_logits_out.release();
     ctx->d_probs_out.release();
     ctx->h_in.release();
@@ -363,6 +430,20 @@ VXS_API int vxs_sample(vxs_ctx* ctx, int rows, int vocab, const float* logits, i
         if ((rc = check_params_host(ctx, rows, params, params_stride, u)) != VXS_OK) return rc;
         if ((rc = check_hist_host(ctx, rows, hist_off, hist_ids)) != VXS_OK) return rc;
         VXS_HIP(ctx, hipSetDevice(ctx->device));
+        if (polled_call(rows, vocab, flags, out_logits != nullptr, out_probs != nullptr)) {
+            vxs::SampleArgs done{};
+            VXS_HIP(ctx, ensure_done(ctx, rows, done));
+            rc = stage_and_launch(ctx, rows, vocab, logits, ld, hist_off, hist_ids, params, params_stride, u, false,
+                                  false, 0, flags, &done);
+            if (rc != VXS_OK) {
+                ctx->done_ready = false;
+                return rc;
+            }
+            if ((rc = wait_done(ctx, done.done_seq)) != VXS_OK) return rc;
+            std::memcpy(out_ids, done.out_ids, sizeof(int32_t) * (size_t)rows);
+            ctx->err.clear();
+            return first_row_error(ctx, out_ids, rows);
+        }
         rc = stage_and_launch(ctx, rows, vocab, logits, ld, hist_off, hist_ids, params, params_stride, u,
                               out_logits != nullptr, out_probs != nullptr, 0, flags);
         if (rc != VXS_OK) return rc;

@@ -34,6 +34,13 @@ struct SampleArgs {
     int32_t* defer_list;  // [rows]
     int32_t* defer_count;
     int32_t* defer_next;
+    // Host-visible completion for small host calls (one workgroup per row): after its row, every
+    // workgroup counts itself in *done_count (device memory, zero between calls); the last one
+    // resets the count and stores done_seq to *done_flag (pinned host memory), which the host
+    // polls instead of synchronising the stream. Unused when done_flag is null.
+    int32_t* done_count;
+    int32_t* done_flag;
+    int32_t done_seq;
 };
 
 enum : int {

@@ -1149,11 +1149,26 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
     }
 }
 
+// The last workgroup of the grid publishes a.done_seq to the host (see SampleArgs::done_flag).
+__device__ __forceinline__ void signal_done(const SampleArgs& a) {
+    __threadfence_system();  // this thread's id store is visible to the host before the count
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int prev = atomicAdd(a.done_count, 1);
+        if (prev == (int)gridDim.x - 1) {
+            *a.done_count = 0;  // the next call (stream-ordered after this one) starts from zero
+            __threadfence_system();
+            __hip_atomic_store(a.done_flag, a.done_seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+}
+
 template <int NC>
 __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<NC>))) void sample_rows_kernel(
     SampleArgs a, int vec) {
     __shared__ RowSmem<NC> sm;
     row_block<NC>(a, vec, blockIdx.x, sm);
+    if (a.done_flag) signal_done(a);
 }
 
 // Four rows per workgroup, one per wave, through the one-wave fast path (vxs_wave.h). A row the
