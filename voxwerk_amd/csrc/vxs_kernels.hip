@@ -143,6 +143,20 @@ struct Blk {
         total = tot;
         return base + incl - v;
     }
+    __device__ __forceinline__ uint64_t excl_scan(uint64_t v, int site, uint64_t& total) const {
+        const uint64_t incl = wave_incl_sum(v);
+        if (lane == 0) slot[site][wv] = readlane64(incl, 63);
+        __syncthreads();
+        uint64_t base = 0, tot = 0;
+#pragma unroll
+        for (int i = 0; i < kWaves; i++) {
+            const uint64_t s = slot[site][i];
+            base += i < wv ? s : 0;
+            tot += s;
+        }
+        total = tot;
+        return base + incl - v;
+    }
     __device__ __forceinline__ double excl_scan(double v, int site, double& total) const {
         const double incl = wave_incl_sum(v);
         if (lane == 0) slot[site][wv] = (uint64_t)__double_as_longlong(readlane_d(incl, 63));
@@ -436,9 +450,11 @@ __device__ __forceinline__ void block_select(const Blk& g, RowSmem<NC>& sm, uint
         const uint32_t ka = s.lkey[a];
         const int ia = s.lidx[a];
         int rank = 0;
+#pragma unroll 8
         for (int b = 0; b < (int)n; b++) {
             const uint32_t kb = s.lkey[b];
-            rank += (kb < ka) || (kb == ka && s.lidx[b] < ia);
+            const int ib = s.lidx[b];
+            rank += (int)((kb < ka) | ((kb == ka) & (ib < ia)));  // bitwise: no branch per comparison
         }
         s.lws[rank] = s.lw[a];
         s.lat[rank] = (int16_t)a;
@@ -480,6 +496,22 @@ template <int NC>
 constexpr int kWavesPerEu = NC <= 3 ? 4 : 1;
 
 // One row by the whole 256-thread workgroup (every thread calls it; it returns uniformly).
+// Left-to-right double sum of x[0..n) (the reference's sequential Sum), reading LDS 8 values at a
+// time so one read latency covers eight additions.
+__device__ __forceinline__ double seq_sum(const double* x, int n) {
+    double s = 0.0;
+    int j = 0;
+    for (; j + 8 <= n; j += 8) {
+        double b[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) b[k] = x[j + k];
+#pragma unroll
+        for (int k = 0; k < 8; k++) s += b[k];
+    }
+    for (; j < n; j++) s += x[j];
+    return s;
+}
+
 template <int NC>
 __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, RowSmem<NC>& sm) {
     using C = Cfg<NC>;
@@ -754,24 +786,53 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
         // ================= exact regime: the reference's sequential fp64 arithmetic =================
         auto& ex = sm.u.ex;
         g.sync();
-        uint32_t base = 0;
+        if constexpr (NC <= 4) {
+            // one scan for every sweep: 16-bit counts per sweep (at most kCandMax candidates)
+            uint64_t mine = 0;
 #pragma unroll
-        for (int c = 0; c < NC; c++) {
-            uint32_t mine = 0;
+            for (int c = 0; c < NC; c++) {
+                uint32_t m = 0;
 #pragma unroll
-            for (int j = 0; j < 4; j++) mine += v[c * 4 + j] != kNegInf ? 1u : 0u;
-            uint32_t total;
-            uint32_t off = base + g.excl_scan(mine, kSiteComp0 + c, total);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int e = c * 4 + j;
-                if (v[e] != kNegInf) {
-                    ex.cx[off] = v[e];
-                    ex.ci[off] = eidx(e);
-                    off++;
-                }
+                for (int j = 0; j < 4; j++) m += v[c * 4 + j] != kNegInf ? 1u : 0u;
+                mine |= (uint64_t)m << (16 * c);
             }
-            base += total;
+            uint64_t total;
+            const uint64_t excl = g.excl_scan(mine, kSiteComp0, total);
+            uint32_t base = 0;
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                uint32_t off = base + (uint32_t)((excl >> (16 * c)) & 0xffffu);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int e = c * 4 + j;
+                    if (v[e] != kNegInf) {
+                        ex.cx[off] = v[e];
+                        ex.ci[off] = eidx(e);
+                        off++;
+                    }
+                }
+                base += (uint32_t)((total >> (16 * c)) & 0xffffu);
+            }
+        } else {
+            uint32_t base = 0;
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                uint32_t mine = 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) mine += v[c * 4 + j] != kNegInf ? 1u : 0u;
+                uint32_t total;
+                uint32_t off = base + g.excl_scan(mine, kSiteComp0 + c, total);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int e = c * 4 + j;
+                    if (v[e] != kNegInf) {
+                        ex.cx[off] = v[e];
+                        ex.ci[off] = eidx(e);
+                        off++;
+                    }
+                }
+                base += total;
+            }
         }
         if (prow)
 #pragma unroll
@@ -783,8 +844,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
         const int n = (int)cnt;
         for (int j = g.t; j < n; j += kT) ex.cp[j] = exp((double)(ex.cx[j] - m));  // Sampler.cs:57
         g.sync();
-        double sum = 0.0;  // sequential in index order                                  :58
-        for (int j = 0; j < n; j++) sum += ex.cp[j];
+        double sum = seq_sum(ex.cp, n);  // sequential in index order                      :58
         g.sync();
         for (int j = g.t; j < n; j += kT) ex.cp[j] = ex.cp[j] / sum;  //                 :60
         g.sync();
@@ -793,9 +853,10 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
             for (int j = g.t; j < n; j += kT) {
                 const double pj = ex.cp[j];
                 int rank = 0;
+#pragma unroll 8
                 for (int l = 0; l < n; l++) {
                     const double pl = ex.cp[l];
-                    rank += (pl < pj) || (pl == pj && l < j);
+                    rank += (int)((pl < pj) | ((pl == pj) & (l < j)));
                 }
                 ex.cs[rank] = (int16_t)j;
             }
@@ -805,36 +866,64 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
             // The largest (p, index) entry is the reference's last sorted position, which its
             // loop (j < n - 1) never visits; masked entries sort first with p = 0 and change
             // nothing. The scan only reads; the removed prefix is zeroed after a barrier.
-            int nrem = n - 1;
-            for (int s = 0; s < n - 1; s++) {
-                cum += ex.cp[ex.cs[s]];
-                if (!(cum <= thr)) {
-                    nrem = s;
-                    break;
+            // cum never decreases until it turns NaN (and then stays NaN), so the first s with
+            // !(cum <= thr) is the number of prefixes with cum <= thr: counted off the additions'
+            // critical path, 8 LDS reads per batch
+            int nrem = 0;
+            for (int s0 = 0; s0 < n - 1 && nrem == s0; s0 += 8) {  // stop after the batch that fails
+                double pb[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) pb[k] = s0 + k < n - 1 ? ex.cp[ex.cs[s0 + k]] : 0.0;
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    cum += pb[k];
+                    nrem += (s0 + k < n - 1 && cum <= thr) ? 1 : 0;
                 }
             }
             g.sync();
             for (int s = g.t; s < nrem; s += kT) ex.cp[ex.cs[s]] = 0.0;
             g.sync();
-            double s2 = 0.0;  // probs.Sum(), sequential
-            for (int j = 0; j < n; j++) s2 += ex.cp[j];
+            double s2 = seq_sum(ex.cp, n);  // probs.Sum(), sequential
             g.sync();
             for (int j = g.t; j < n; j += kT) ex.cp[j] = ex.cp[j] / s2;
             g.sync();
         }
-        // inverse-CDF draw in index order                                               :77-87
+        // inverse-CDF draw in index order. The accumulation is sequential (skipped entries add 0,
+        // which leaves acc unchanged) and acc never decreases until it turns NaN, after which it
+        // stays NaN; so the reference's first index with u < acc is the number of prefixes with
+        // acc <= u, provided that number is below the first NaN prefix. Both counts are taken off
+        // the critical path of the additions.                                             :77-87
         double acc = 0.0;
-        int last = 0, pick = -1;
-        for (int j = 0; j < n; j++) {
-            const double pj = ex.cp[j];
-            if (pj <= 0.0) continue;
-            acc += pj;
-            last = ex.ci[j];
-            if (u < acc) {
-                pick = last;
-                break;
+        int below_u = 0, nan_prefixes = 0, lastj = -1, scanned = 0;
+        for (int j0 = 0; j0 < n && below_u == j0 && nan_prefixes == 0; j0 += 8) {  // stop after the deciding batch
+            scanned = min(n, j0 + 8);
+            double pb[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const double pj = j0 + k < n ? ex.cp[j0 + k] : 0.0;
+                const bool take = !(pj <= 0.0);  // NaN is not skipped, like the reference's `<= 0` test
+                pb[k] = take ? pj : 0.0;
+                lastj = take ? j0 + k : lastj;
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                acc += pb[k];
+                below_u += (j0 + k < n && acc <= u) ? 1 : 0;
+                nan_prefixes += (j0 + k < n && acc != acc) ? 1 : 0;
             }
         }
+        // Prefixes turn NaN for good at first_nan. With the early stop, `last` may not have seen
+        // the entries after the deciding batch; it only matters without a pick, and then either
+        // every batch was scanned or a NaN prefix appeared, after which the reference keeps
+        // visiting entries: `last` is finished over all of them for that case.
+        const int first_nan = nan_prefixes > 0 ? scanned - nan_prefixes : n;
+        int pick = -1;
+        if (below_u < first_nan) {
+            pick = ex.ci[below_u];
+        } else if (nan_prefixes > 0) {
+            for (int j = 0; j < n; j++) lastj = !(ex.cp[j] <= 0.0) ? j : lastj;
+        }
+        const int last = lastj >= 0 ? ex.ci[lastj] : 0;
         if (g.t == 0) a.out_ids[r] = pick >= 0 ? pick : last;
         if (prow)
             for (int j = g.t; j < n; j += kT) prow[ex.ci[j]] = ex.cp[j];
