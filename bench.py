@@ -48,6 +48,37 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def native_latency(b, iters):
+    """Host-to-host latency of vxs_sample timed by the native caller built next to the library (the
+    view of a P/Invoke caller), on the batch `b`; None when the program is missing or fails."""
+    import subprocess
+    import tempfile
+
+    import numpy as np
+
+    exe = os.path.join(REPO, "voxwerk_amd", "lib", "vxs_latency")
+    if not os.path.exists(exe):
+        return None
+    rows, vocab = b.logits.shape
+    hlen = int(b.hist_off[1] - b.hist_off[0]) if b.hist_off is not None else 0
+    params = np.broadcast_to(b.params, (rows,)) if b.params.size == 1 else b.params
+    with tempfile.NamedTemporaryFile(suffix=".bin", delete=False) as f:
+        f.write(np.array([rows, vocab, hlen], np.int32).tobytes())
+        f.write(np.ascontiguousarray(b.logits, np.float32).tobytes())
+        f.write(np.ascontiguousarray(b.hist_ids[: rows * hlen], np.int32).tobytes())
+        f.write(np.ascontiguousarray(params).tobytes())
+        f.write(np.ascontiguousarray(b.u, np.float64).tobytes())
+        path = f.name
+    try:
+        p = subprocess.run([exe, path, str(iters)], capture_output=True, text=True, timeout=120)
+        if p.returncode != 0:
+            log(f"[bench] native latency probe failed: {p.stderr.strip()[:200]}")
+            return None
+        return json.loads(p.stdout.strip().splitlines()[-1])
+    finally:
+        os.unlink(path)
+
+
 def read_traffic():
     """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, or None."""
     try:
@@ -263,7 +294,11 @@ def main() -> int:
     if lat:
         lat = np.sort(np.array(lat)) / 1e3
         p50, p99 = round(float(lat[len(lat) // 2]), 2), round(float(lat[int(len(lat) * 0.99)]), 2)
-        log(f"[bench] talker step 1x3072 host-to-host: p50 {p50:.1f} us, p99 {p99:.1f} us")
+        log(f"[bench] talker step 1x3072 host-to-host from Python: p50 {p50:.1f} us, p99 {p99:.1f} us")
+    native = native_latency(b1, args.latency_steps) if args.latency_steps > 0 else None
+    if native:
+        log(f"[bench] talker step 1x3072 host-to-host from native code: p50 {native['p50_us']:.1f} us, "
+            f"p99 {native['p99_us']:.1f} us")
 
     cpu = None
     parity = None
@@ -353,7 +388,14 @@ def main() -> int:
         },
         "hbm_gbps": round(gbps, 1),
         "hbm_pct_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
-        "latency_1row_us": {"p50": p50, "p99": p99, "workload": "talker_step 1x3072 host-to-host"},
+        "latency_1row_us": {
+            "p50": native["p50_us"] if native else p50,
+            "p99": native["p99_us"] if native else p99,
+            "caller": "native C++ through the C ABI (voxwerk_amd/lib/vxs_latency)" if native else "Python ctypes",
+            "python_p50": p50,
+            "python_p99": p99,
+            "workload": "talker_step 1x3072 host-to-host (host logits in, host id out)",
+        },
         "roofline": {
             "bound": "hbm",
             "achieved": round(gbps, 1),

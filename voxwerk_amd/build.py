@@ -63,6 +63,15 @@ def build_selfcheck() -> str:
     return out
 
 
+def build_latency() -> str:
+    """Native caller that times vxs_sample host to host (run by bench.py)."""
+    out = os.path.join(LIB, "vxs_latency")
+    _run(["g++", "-O2", "-std=c++17", "-Wall", f"-I{INCLUDE}", "-o", out + ".tmp", os.path.join(CSRC, "vxs_latency.cpp"),
+          f"-L{LIB}", "-lvxs", "-Wl,-rpath,$ORIGIN"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build_synth() -> str:
     os.makedirs(LIB, exist_ok=True)
     out = os.path.join(LIB, "libvxs_synth.so")
@@ -86,6 +95,7 @@ def build_all(with_tests: bool = True) -> None:
     build_synth()
     build_hip()
     build_selfcheck()
+    build_latency()
     if with_tests and os.path.exists(os.path.join(REPO, "tests", "cpp", "test_facade.cpp")):
         build_facade_test()
 
