@@ -219,6 +219,93 @@ __device__ __forceinline__ float key2f(uint32_t k) {
     return __uint_as_float(u);
 }
 
+// ---- sequential phases of the exact regime (the reference's fp64 loops, Sampler.cs:58-87) ----
+// They run redundantly in every thread on LDS broadcast reads; LDS is read 8 entries at a time so
+// one read latency covers eight steps, and the steps are branch-free.
+
+// Left-to-right double sum of x[0..n) (the reference's sequential Sum).
+__device__ __forceinline__ double seq_sum(const double* x, int n) {
+    double s = 0.0;
+    int j = 0;
+    for (; j + 8 <= n; j += 8) {
+        double b[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) b[k] = x[j + k];
+#pragma unroll
+        for (int k = 0; k < 8; k++) s += b[k];
+    }
+    for (; j < n; j++) s += x[j];
+    return s;
+}
+
+// Top-p cut over the (p, index)-sorted order (order[s] = entry at sorted position s): the number
+// of leading positions, among the first n - 1, whose running sum stays <= thr (Sampler.cs:66-73).
+// The running sum never decreases until it turns NaN (and stays NaN), so the reference's first
+// position with !(cum <= thr) equals the number of prefixes with cum <= thr, counted off the
+// critical path of the additions; the scan stops after the deciding batch.
+__device__ __forceinline__ int seq_topp_cut(const double* p, const int16_t* order, int n, double thr) {
+    double cum = 0.0;
+    int nrem = 0;
+    for (int s0 = 0; s0 < n - 1 && nrem == s0; s0 += 8) {
+        double pb[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) pb[k] = s0 + k < n - 1 ? p[order[s0 + k]] : 0.0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            cum += pb[k];
+            nrem += (s0 + k < n - 1 && cum <= thr) ? 1 : 0;
+        }
+    }
+    return nrem;
+}
+
+// Inverse-CDF draw in index order over p[0..n) with ids id[0..n) (Sampler.cs:77-87): the first
+// entry whose running sum exceeds u, skipping entries with p <= 0 (NaN is not skipped); without
+// one, the last entry visited (0 when none). Skipped entries add 0, which leaves the running sum
+// unchanged, and it never decreases until it turns NaN, so the first crossing is the number of
+// prefixes <= u, provided that is below the first NaN prefix.
+__device__ __forceinline__ int seq_draw(const double* p, const int32_t* id, int n, double u) {
+    double acc = 0.0;
+    int below_u = 0, nan_prefixes = 0, lastj = -1, scanned = 0;
+    for (int j0 = 0; j0 < n && below_u == j0 && nan_prefixes == 0; j0 += 8) {
+        scanned = min(n, j0 + 8);
+        double pb[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const double pj = j0 + k < n ? p[j0 + k] : 0.0;
+            const bool take = !(pj <= 0.0);
+            pb[k] = take ? pj : 0.0;
+            lastj = take ? j0 + k : lastj;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            acc += pb[k];
+            below_u += (j0 + k < n && acc <= u) ? 1 : 0;
+            nan_prefixes += (j0 + k < n && acc != acc) ? 1 : 0;
+        }
+    }
+    // After an early stop `lastj` may have missed later entries; it only matters without a pick,
+    // and then every batch was scanned or a NaN prefix appeared (the reference keeps visiting
+    // entries after it): `lastj` is finished over all entries in that case.
+    const int first_nan = nan_prefixes > 0 ? scanned - nan_prefixes : n;
+    if (below_u < first_nan) return id[below_u];
+    if (nan_prefixes > 0)
+        for (int j = 0; j < n; j++) lastj = !(p[j] <= 0.0) ? j : lastj;
+    return lastj >= 0 ? id[lastj] : 0;
+}
+
+// Stable ascending (p, index) rank of entry j among p[0..n).
+__device__ __forceinline__ int seq_rank(const double* p, int n, int j) {
+    const double pj = p[j];
+    int rank = 0;
+#pragma unroll 8
+    for (int l = 0; l < n; l++) {
+        const double pl = p[l];
+        rank += (int)((pl < pj) | ((pl == pj) & (l < j)));
+    }
+    return rank;
+}
+
 // Nucleus mass of a weight q in [0, 1]: fl32(fl32(q + Cb) - Cb) with Cb = 2^(23 - F), a multiple of
 // 2^-F within 1.5 ulp of q (fl32(q + Cb) >= Cb has an ulp of at least 2^-F; below Cb the subtraction
 // is exact, and every fp32 value at or above Cb is a multiple of 2^-F). Sums of up to 2^(53-F) such

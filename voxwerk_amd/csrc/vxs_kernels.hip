@@ -496,22 +496,6 @@ template <int NC>
 constexpr int kWavesPerEu = NC <= 3 ? 4 : 1;
 
 // One row by the whole 256-thread workgroup (every thread calls it; it returns uniformly).
-// Left-to-right double sum of x[0..n) (the reference's sequential Sum), reading LDS 8 values at a
-// time so one read latency covers eight additions.
-__device__ __forceinline__ double seq_sum(const double* x, int n) {
-    double s = 0.0;
-    int j = 0;
-    for (; j + 8 <= n; j += 8) {
-        double b[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) b[k] = x[j + k];
-#pragma unroll
-        for (int k = 0; k < 8; k++) s += b[k];
-    }
-    for (; j < n; j++) s += x[j];
-    return s;
-}
-
 template <int NC>
 __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, RowSmem<NC>& sm) {
     using C = Cfg<NC>;
@@ -850,36 +834,13 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
         g.sync();
         if (topp) {  //                                                                 :62-75
             // stable ascending (p, index) order of the candidates (slot order == index order)
-            for (int j = g.t; j < n; j += kT) {
-                const double pj = ex.cp[j];
-                int rank = 0;
-#pragma unroll 8
-                for (int l = 0; l < n; l++) {
-                    const double pl = ex.cp[l];
-                    rank += (int)((pl < pj) | ((pl == pj) & (l < j)));
-                }
-                ex.cs[rank] = (int16_t)j;
-            }
+            for (int j = g.t; j < n; j += kT) ex.cs[seq_rank(ex.cp, n, j)] = (int16_t)j;
             g.sync();
             const double thr = (double)(1.0f - P.top_p);
-            double cum = 0.0;
             // The largest (p, index) entry is the reference's last sorted position, which its
             // loop (j < n - 1) never visits; masked entries sort first with p = 0 and change
             // nothing. The scan only reads; the removed prefix is zeroed after a barrier.
-            // cum never decreases until it turns NaN (and then stays NaN), so the first s with
-            // !(cum <= thr) is the number of prefixes with cum <= thr: counted off the additions'
-            // critical path, 8 LDS reads per batch
-            int nrem = 0;
-            for (int s0 = 0; s0 < n - 1 && nrem == s0; s0 += 8) {  // stop after the batch that fails
-                double pb[8];
-#pragma unroll
-                for (int k = 0; k < 8; k++) pb[k] = s0 + k < n - 1 ? ex.cp[ex.cs[s0 + k]] : 0.0;
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    cum += pb[k];
-                    nrem += (s0 + k < n - 1 && cum <= thr) ? 1 : 0;
-                }
-            }
+            const int nrem = seq_topp_cut(ex.cp, ex.cs, n, thr);
             g.sync();
             for (int s = g.t; s < nrem; s += kT) ex.cp[ex.cs[s]] = 0.0;
             g.sync();
@@ -888,43 +849,8 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
             for (int j = g.t; j < n; j += kT) ex.cp[j] = ex.cp[j] / s2;
             g.sync();
         }
-        // inverse-CDF draw in index order. The accumulation is sequential (skipped entries add 0,
-        // which leaves acc unchanged) and acc never decreases until it turns NaN, after which it
-        // stays NaN; so the reference's first index with u < acc is the number of prefixes with
-        // acc <= u, provided that number is below the first NaN prefix. Both counts are taken off
-        // the critical path of the additions.                                             :77-87
-        double acc = 0.0;
-        int below_u = 0, nan_prefixes = 0, lastj = -1, scanned = 0;
-        for (int j0 = 0; j0 < n && below_u == j0 && nan_prefixes == 0; j0 += 8) {  // stop after the deciding batch
-            scanned = min(n, j0 + 8);
-            double pb[8];
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const double pj = j0 + k < n ? ex.cp[j0 + k] : 0.0;
-                const bool take = !(pj <= 0.0);  // NaN is not skipped, like the reference's `<= 0` test
-                pb[k] = take ? pj : 0.0;
-                lastj = take ? j0 + k : lastj;
-            }
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                acc += pb[k];
-                below_u += (j0 + k < n && acc <= u) ? 1 : 0;
-                nan_prefixes += (j0 + k < n && acc != acc) ? 1 : 0;
-            }
-        }
-        // Prefixes turn NaN for good at first_nan. With the early stop, `last` may not have seen
-        // the entries after the deciding batch; it only matters without a pick, and then either
-        // every batch was scanned or a NaN prefix appeared, after which the reference keeps
-        // visiting entries: `last` is finished over all of them for that case.
-        const int first_nan = nan_prefixes > 0 ? scanned - nan_prefixes : n;
-        int pick = -1;
-        if (below_u < first_nan) {
-            pick = ex.ci[below_u];
-        } else if (nan_prefixes > 0) {
-            for (int j = 0; j < n; j++) lastj = !(ex.cp[j] <= 0.0) ? j : lastj;
-        }
-        const int last = lastj >= 0 ? ex.ci[lastj] : 0;
-        if (g.t == 0) a.out_ids[r] = pick >= 0 ? pick : last;
+        const int pick = seq_draw(ex.cp, ex.ci, n, u);  // inverse-CDF draw in index order   :77-87
+        if (g.t == 0) a.out_ids[r] = pick;
         if (prow)
             for (int j = g.t; j < n; j += kT) prow[ex.ci[j]] = ex.cp[j];
         return;

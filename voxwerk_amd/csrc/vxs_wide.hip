@@ -230,56 +230,27 @@ __device__ __forceinline__ int exact_block(const BlkW& g, WideSmem& s, int n, fl
     auto& ex = s.ex;
     for (int j = g.t; j < n; j += kTW) ex.cp[j] = exp((double)(ex.cx[j] - m));  // Sampler.cs:57
     __syncthreads();
-    double sum = 0.0;  // sequential in index order                                     :58
-    for (int j = 0; j < n; j++) sum += ex.cp[j];
+    const double sum = seq_sum(ex.cp, n);  // sequential in index order                  :58
     __syncthreads();
     for (int j = g.t; j < n; j += kTW) ex.cp[j] = ex.cp[j] / sum;  //                   :60
     __syncthreads();
     if (topp) {  //                                                                    :62-75
-        for (int j = g.t; j < n; j += kTW) {
-            const double pj = ex.cp[j];
-            int rank = 0;
-            for (int l = 0; l < n; l++) {
-                const double pl = ex.cp[l];
-                rank += (pl < pj) || (pl == pj && l < j);
-            }
-            ex.cs[rank] = (int16_t)j;
-        }
+        for (int j = g.t; j < n; j += kTW) ex.cs[seq_rank(ex.cp, n, j)] = (int16_t)j;
         __syncthreads();
-        const double thr = (double)(1.0f - top_p);
-        double cum = 0.0;
-        int nrem = n - 1;  // the last sorted position is never removed (loop j < n - 1)
-        for (int q = 0; q < n - 1; q++) {
-            cum += ex.cp[ex.cs[q]];
-            if (!(cum <= thr)) {
-                nrem = q;
-                break;
-            }
-        }
+        // the last sorted position is never removed (the reference's loop runs j < n - 1)
+        const int nrem = seq_topp_cut(ex.cp, ex.cs, n, (double)(1.0f - top_p));
         __syncthreads();
         for (int q = g.t; q < nrem; q += kTW) ex.cp[ex.cs[q]] = 0.0;
         __syncthreads();
-        double s2 = 0.0;
-        for (int j = 0; j < n; j++) s2 += ex.cp[j];
+        const double s2 = seq_sum(ex.cp, n);
         __syncthreads();
         for (int j = g.t; j < n; j += kTW) ex.cp[j] = ex.cp[j] / s2;
         __syncthreads();
     }
-    double acc = 0.0;  // inverse-CDF draw in index order                               :77-87
-    int last = 0, pick = -1;
-    for (int j = 0; j < n; j++) {
-        const double pj = ex.cp[j];
-        if (pj <= 0.0) continue;
-        acc += pj;
-        last = ex.ci[j];
-        if (u < acc) {
-            pick = last;
-            break;
-        }
-    }
+    const int pick = seq_draw(ex.cp, ex.ci, n, u);  // inverse-CDF draw in index order    :77-87
     if (prow)
         for (int j = g.t; j < n; j += kTW) prow[ex.ci[j]] = ex.cp[j];
-    return pick >= 0 ? pick : last;
+    return pick;
 }
 
 __global__ __launch_bounds__(kTW) void sample_wide_kernel(SampleArgs a, int vec) {
@@ -616,7 +587,8 @@ __global__ __launch_bounds__(kTW) void sample_wide_kernel(SampleArgs a, int vec)
                 xj = s.ex.cx[g.t];
             }
             int rank = 0;
-            for (int l = 0; l < n; l++) rank += s.ex.ci[l] < ij;
+#pragma unroll 8
+            for (int l = 0; l < n; l++) rank += s.ex.ci[l] < ij;  // batched LDS reads
             __syncthreads();
             if (g.t < n) {
                 s.ex.ci[rank] = ij;
