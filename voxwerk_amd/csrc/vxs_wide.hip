@@ -38,23 +38,36 @@ constexpr int kPerL = kCapW / 64;  // ... per lane
 constexpr int kKMax = 256;        // largest top-k of the streaming path
 constexpr int kCandW = 256;       // exact-regime capacity
 constexpr int kRB = 256;          // radix buckets (8-bit digits)
+// zero words after the history bitmap: a sweep's lanes past the row end (up to 255 entries) read
+// bitmap words within the allocation
+constexpr int kBmPad = 8;
+// out_ids value the ordered kernel leaves for a row that the general kernel must serve
+constexpr int32_t kPendingId = INT32_MIN;
 
 struct WideSmem {
     uint32_t wkey[kWW][kCapW];  // per-wave candidate keys (f2key of the value)
     int32_t widx[kWW][kCapW];   // per-wave candidate indices
+    // The radix histograms are done with before the exact-regime arrays are filled, so the two
+    // share their storage: with the history bitmap of a 151936-entry row this keeps a workgroup
+    // within 40 KB of LDS, four workgroups (16 waves) per CU.
     union {
-        uint32_t hcnt[kRB];
-        double hmass[kRB];
-    } h;
-    struct {
-        float cx[kCandW];
-        int32_t ci[kCandW];
-        double cp[kCandW];
-        int16_t cs[kCandW];
-    } ex;
+        union {
+            uint32_t hcnt[kRB];
+            double hmass[kRB];
+        } h;
+        struct {
+            float cx[kCandW];
+            int32_t ci[kCandW];
+            double cp[kCandW];  // also the (d, index) sort keys before the probabilities
+            int16_t cs[kCandW];
+        } ex;
+    };
     uint64_t slot[4][kWW];
     int32_t wcnt[kWW];  // per-wave candidate counts after pass A (-1: the wave's buffer overflowed)
+    int32_t wcomp[kWW]; // per-wave: the buffer was compacted at least once (ordered kernel)
     uint32_t tau_key;   // the largest k-th largest any wave has found so far (a shared lower bound)
+    uint32_t kth_key;   // ordered kernel: the row's k-th largest (0 without top-k) ...
+    float mx;           // ... and its maximum
     int32_t n;          // exact-regime candidates
 };
 
@@ -163,8 +176,31 @@ __device__ __forceinline__ void for_row(const float* __restrict__ xrow, int V, i
     }
 }
 
-// k-th largest (1-based, with multiplicity) of a wave's n >= k buffered keys: the largest key K
-// with at least k keys >= K, by bisection over [min key, max key]; wave-local, no LDS atomics.
+// Orders a wave's LDS accesses: its earlier writes are visible to all its lanes afterwards.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The largest key K with at least k of the wave's register-held keys >= K (the k-th largest with
+// multiplicity), by bisection over [lo, hi], the smallest and largest valid key. Empty slots hold
+// 0, below every valid key. Counts come from ballots, so a step costs one compare per slot.
+template <int N>
+__device__ __forceinline__ uint32_t wave_kth_regs(const uint32_t (&kk)[N], uint32_t lo, uint32_t hi, int k) {
+#pragma unroll 1
+    while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo + 1) >> 1);
+        int c = 0;
+#pragma unroll
+        for (int q = 0; q < N; q++) c += __builtin_popcountll(__ballot(kk[q] >= mid));
+        if (c >= k) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+// k-th largest (1-based, with multiplicity) of a wave's n >= k buffered keys; wave-local.
 __device__ __forceinline__ uint32_t wave_kth(const uint32_t* keys, int lane, int n, int k) {
     uint32_t kk[kPerL];
     uint32_t lo = 0xffffffffu, hi = 0;
@@ -177,18 +213,7 @@ __device__ __forceinline__ uint32_t wave_kth(const uint32_t* keys, int lane, int
             hi = max(hi, kk[q]);
         }
     }
-    lo = wave_umin(lo);
-    hi = wave_umax(hi);
-#pragma unroll 1
-    while (lo < hi) {
-        const uint32_t mid = lo + ((hi - lo + 1) >> 1);
-        uint32_t c = 0;
-#pragma unroll
-        for (int q = 0; q < kPerL; q++) c += kk[q] >= mid ? 1u : 0u;  // empty slots hold 0 < mid
-        if ((int)wave_sum(c) >= k) lo = mid;
-        else hi = mid - 1;
-    }
-    return lo;
+    return wave_kth_regs(kk, wave_umin(lo), wave_umax(hi), k);
 }
 
 // Keep a wave's buffered entries with key >= kmin (order kept). Returns the new count.
@@ -201,9 +226,7 @@ __device__ __forceinline__ int wave_filter(uint32_t* keys, int32_t* idx, int lan
         kk[q] = j < n ? keys[j] : 0;
         ii[q] = j < n ? idx[j] : 0;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wave_sync();
     uint32_t m = 0;
 #pragma unroll
     for (int q = 0; q < kPerL; q++) {
@@ -217,9 +240,7 @@ __device__ __forceinline__ int wave_filter(uint32_t* keys, int32_t* idx, int lan
         }
         m += (uint32_t)__builtin_popcountll(bal);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wave_sync();
     return (int)m;
 }
 
@@ -253,17 +274,63 @@ __device__ __forceinline__ int exact_block(const BlkW& g, WideSmem& s, int n, fl
     return pick;
 }
 
+// fl32(1/T) of a row, 1 for greedy rows                                     Sampler.cs:39-40
+__device__ __forceinline__ float row_inv_temp(const vxs_params& P) {
+    return !P.do_sample ? 1.0f : (P.temperature == 1.0f ? 1.0f : 1.0f / P.temperature);
+}
+
+// Rows the ordered kernel serves: sampled, 0 < k <= kKMax and k < V, 1/T finite and positive, and
+// no penalty or one that never raises a value (rho >= 1). For them fl(x * 1/T) bounds the
+// transformed value from above and is monotone in the raw value x.
+__device__ __forceinline__ bool row_ordered(const SampleArgs& a, const vxs_params& P) {
+    if (a.kflags & KF_STOP_AFTER_PENALTY) return false;
+    const float invT = row_inv_temp(P);
+    const bool has_pen = P.rep_penalty != 1.0f && a.hist_off != nullptr;
+    return P.do_sample && P.top_k > 0 && P.top_k <= kKMax && P.top_k < a.vocab && invT > 0.0f &&
+           invT < kPosInf && (!has_pen || P.rep_penalty >= 1.0f);
+}
+
+// The LDS bitmap of row r's history ids (S1), with kBmPad zero words after it. All threads call
+// it; false (with the error id written) when an id lies outside [0, V).
+__device__ __forceinline__ bool build_bitmap(const BlkW& g, const SampleArgs& a, int r, int V, uint32_t* bm) {
+    const int words = ((V + 31) >> 5) + kBmPad;
+    for (int w = g.t; w < words; w += kTW) bm[w] = 0;
+    __syncthreads();
+    const int h0 = a.hist_off[r], h1 = a.hist_off[r + 1];
+    bool bad = false;
+    for (int hb = h0; hb < h1; hb += 4 * kTW) {  // four ids per thread in flight
+        int id[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int h = hb + k * kTW + g.t;
+            id[k] = h < h1 ? a.hist_ids[h] : 0;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (hb + k * kTW + g.t >= h1) continue;
+            if ((unsigned)id[k] >= (unsigned)V) bad = true;
+            else atomicOr(&bm[id[k] >> 5], 1u << (id[k] & 31));
+        }
+    }
+    if (g.any(bad)) {
+        if (g.t == 0) a.out_ids[r] = VXS_ERR_ID_OUT_OF_RANGE;
+        return false;
+    }
+    return true;
+}
+
 __global__ __launch_bounds__(kTW) void sample_wide_kernel(SampleArgs a, int vec) {
     extern __shared__ uint32_t bm_dyn[];  // penalised-id bitmap, ceil(vocab / 32) words
     __shared__ WideSmem s;
     BlkW g;
     g.t = threadIdx.x;
     g.lane = g.t & 63;
-    g.wv = g.t >> 6;
+    g.wv = __builtin_amdgcn_readfirstlane(g.t >> 6);  // wave-uniform: wave ranges live in SGPRs
     g.s = &s;
     const int r = blockIdx.x;
     const int V = a.vocab;
     const vxs_params P = a.params[(int64_t)r * a.params_stride];
+    if (row_ordered(a, P) && a.out_ids[r] != kPendingId) return;  // served by the ordered kernel
     const float* __restrict__ xrow = a.logits + (int64_t)r * a.ld;
     float* orow = a.out_logits ? a.out_logits + (int64_t)r * V : nullptr;
     double* prow = a.out_probs ? a.out_probs + (int64_t)r * V : nullptr;
@@ -276,20 +343,7 @@ __global__ __launch_bounds__(kTW) void sample_wide_kernel(SampleArgs a, int vec)
     X.rinv = 1.0f / P.rep_penalty;
     X.fastdiv = __builtin_fabsf(P.rep_penalty) >= 0x1p-60f && __builtin_fabsf(P.rep_penalty) <= 0x1p60f;
     if (P.rep_penalty != 1.0f && a.hist_off != nullptr) {
-        const int words = (V + 31) >> 5;
-        for (int w = g.t; w < words; w += kTW) bm_dyn[w] = 0;
-        __syncthreads();
-        const int h0 = a.hist_off[r], h1 = a.hist_off[r + 1];
-        bool bad = false;
-        for (int h = h0 + g.t; h < h1; h += kTW) {
-            const int id = a.hist_ids[h];
-            if ((unsigned)id >= (unsigned)V) bad = true;
-            else atomicOr(&bm_dyn[id >> 5], 1u << (id & 31));
-        }
-        if (g.any(bad)) {
-            if (g.t == 0) a.out_ids[r] = VXS_ERR_ID_OUT_OF_RANGE;
-            return;
-        }
+        if (!build_bitmap(g, a, r, V, bm_dyn)) return;
         X.bm = bm_dyn;
     }
     if (stop_pen) {  // ApplyRepetitionPenalty alone: write the penalised row
@@ -307,7 +361,7 @@ __global__ __launch_bounds__(kTW) void sample_wide_kernel(SampleArgs a, int vec)
     X.keep = P.keep_id;
     X.ban = P.ban_id;
     const bool greedy = !P.do_sample;
-    X.invT = greedy ? 1.0f : (P.temperature == 1.0f ? 1.0f : 1.0f / P.temperature);
+    X.invT = row_inv_temp(P);
     if (g.t == 0) s.tau_key = 0;
     __syncthreads();
 
@@ -430,9 +484,7 @@ __global__ __launch_bounds__(kTW) void sample_wide_kernel(SampleArgs a, int vec)
                 }
                 wn += __builtin_popcountll(bal);
                 if (wn > kCapW - 64) {  // room for less than one more slot: raise tau and compact
-                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                    __builtin_amdgcn_wave_barrier();
-                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    wave_sync();
                     const uint32_t kth = wave_kth(wkey, g.lane, wn, K);
                     wn = wave_filter(wkey, widx, g.lane, wn, kth);
                     tau = fmaxf(tau, key2f(kth));
@@ -818,13 +870,416 @@ __global__ __launch_bounds__(kTW) void sample_wide_kernel(SampleArgs a, int vec)
     }
 }
 
+
+// The smallest float x with fl(x * invT) >= tau, for finite tau and invT in (0, inf): then
+// x >= xt  <=>  fl(x * invT) >= tau  for every x (fl(x * invT) is monotone in x, NaN fails both).
+// Found from the quotient by a few steps in key order, with a bisection as the fallback.
+__device__ __forceinline__ float x_threshold(float tau, float invT) {
+    auto ok = [&](uint32_t k) { return key2f(k) * invT >= tau; };
+    uint32_t k = f2key(tau / invT);
+    if (k >= 0xff800001u) k = 0xff800000u;  // +inf at most
+    if (k <= 0x007fffffu) k = 0x00800000u;  // above -inf
+#pragma unroll 1
+    for (int i = 0; i < 4 && ok(k - 1) && k > 0x00800000u; i++) k--;
+#pragma unroll 1
+    for (int i = 0; i < 4 && !ok(k); i++) k++;
+    if (!(ok(k) && (k == 0x00800000u || !ok(k - 1)))) {  // not settled: bisect over [-FLT_MAX, +inf]
+        uint32_t lo = 0x00800000u, hi = 0xff800000u;  // ok(hi) holds (tau is finite)
+#pragma unroll 1
+        while (lo < hi) {
+            const uint32_t mid = lo + ((hi - lo) >> 1);
+            if (ok(mid)) hi = mid;
+            else lo = mid + 1;
+        }
+        k = lo;
+    }
+    return key2f(k);
+}
+
+// =====================================================================================
+// The ordered kernel: the rows row_ordered() selects, in one read of the row.
+//
+// Pass A: each wave streams its quarter of the row and keeps a buffer of raw values and indices.
+// The exact transformed value v = fl(pen(x) * 1/T) is at most fl(x * 1/T), which is monotone in x,
+// so an entry joins the buffer when fl(x * 1/T) >= tau; whenever the buffer cannot take a sweep's
+// entries, the exact values of the buffered entries are formed and the buffer is cut to those >=
+// its k-th largest, which becomes tau (a lower bound of the row's k-th largest, shared between the
+// waves). Sweeps that suppression or the range end touch apply the full transform per entry. NaN
+// reaches the NaN-propagating maximum M of the raw values; fl(M * 1/T) = +inf sends the row
+// through an exact check with the full transform (the penalty may have lowered that value).
+// Tail: wave 0 finds the k-th largest of the four buffers by bisection and extracts the
+// candidates; all waves rank them by index and by (d, index), d = v - max; wave 0 runs the
+// reference's sequential fp64 arithmetic (S6-S8, Sampler.cs:51-87). The (d, index) order is the
+// reference's (p, index) order whenever each adjacent pair is in (p, index) order (p = exp(d) / sum
+// never decreases with d for a monotone exp); otherwise the candidates are ranked by p directly.
+// Rows that end with too many tied candidates are marked kPendingId for the general kernel.
+// =====================================================================================
+__global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void sample_wide_ordered_kernel(
+    SampleArgs a, int vec) {
+    extern __shared__ uint32_t bm_dyn[];
+    __shared__ WideSmem s;
+    BlkW g;
+    g.t = threadIdx.x;
+    g.lane = g.t & 63;
+    g.wv = __builtin_amdgcn_readfirstlane(g.t >> 6);
+    g.s = &s;
+    const int r = blockIdx.x;
+    const int V = a.vocab;
+    const vxs_params P = a.params[(int64_t)r * a.params_stride];
+    if (!row_ordered(a, P)) return;  // the general kernel serves it
+    const float* __restrict__ xrow = a.logits + (int64_t)r * a.ld;
+    const float invT = row_inv_temp(P);
+    const int K = P.top_k;
+
+    RowX X;
+    X.bm = nullptr;
+    X.rho = P.rep_penalty;
+    X.rinv = 1.0f / P.rep_penalty;
+    X.fastdiv = __builtin_fabsf(P.rep_penalty) >= 0x1p-60f && __builtin_fabsf(P.rep_penalty) <= 0x1p60f;
+    if (P.rep_penalty != 1.0f && a.hist_off != nullptr) {
+        if (!build_bitmap(g, a, r, V, bm_dyn)) return;
+        X.bm = bm_dyn;
+    }
+    X.sb = max(P.supp_begin, 0);
+    X.se = min(P.supp_end, V);
+    if (!(P.supp_begin < P.supp_end)) X.sb = X.se = 0;
+    X.keep = P.keep_id;
+    X.ban = P.ban_id;
+    X.invT = invT;
+    if (g.t == 0) s.tau_key = 0;
+    __syncthreads();
+
+    // ---- pass A
+    const int Q = ((V + kTW * 4 - 1) / (kTW * 4)) * 256;  // a wave's range, a multiple of 256
+    const int lo = g.wv * Q, hi = min(V, lo + Q);
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    // raw buffer loads bounded by the row: lanes past its end read zeros instead of faulting
+    const __amdgpu_buffer_rsrc_t rowbuf =
+        __builtin_amdgcn_make_buffer_rsrc((void*)xrow, (short)0, V * (int)sizeof(float), 0x00020000);
+    auto load4 = [&](int base) -> f4 {
+        return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rowbuf, (base + 4 * g.lane) * 4, 0, 2));
+    };
+    uint32_t* wkey = s.wkey[g.wv];
+    int32_t* widx = s.widx[g.wv];
+    bool collect = true;            // false once the wave stops collecting (the general kernel then serves the row)
+    int wn = 0;                     // wave-uniform buffer fill
+    float tau = -3.402823466e38f;   // entries with fl(x * 1/T) < tau are not candidates ...
+    float xt = x_threshold(tau, invT);  // ... which is x < xt
+    float M = kNegInf;              // NaN-propagating maximum of the raw entries
+    bool compacted = false;
+    // The exact value of entry i: the full transform (penalty, suppression, temperature); entries
+    // past the wave's range (the zeros loaded beyond the row end) are -inf.
+    auto vexact = [&](int i, float x) -> float { return i < hi ? X(i, x) : kNegInf; };
+    // Keep the buffered entries whose exact value is >= the k-th largest exact value buffered (or
+    // the shared bound, if larger); tau rises to it. With fewer than k finite values buffered the
+    // wave stops collecting.
+    auto compact = [&]() {
+        wave_sync();
+        uint32_t kk[kPerL];
+        float xr[kPerL];
+        int32_t ii[kPerL];
+        uint32_t klo = 0xffffffffu, khi = 0;
+        int nf = 0;
+#pragma unroll
+        for (int q = 0; q < kPerL; q++) {
+            const int j = g.lane + 64 * q;
+            xr[q] = __uint_as_float(wkey[j]);
+            ii[q] = widx[j];
+            const bool in = j < wn;
+            const float v = vexact(in ? ii[q] : lo, xr[q]);
+            const bool fin = in && v > kNegInf;
+            kk[q] = fin ? f2key(v) : 0u;
+            klo = fin ? min(klo, kk[q]) : klo;
+            khi = fin ? max(khi, kk[q]) : khi;
+            nf += __builtin_popcountll(__ballot(fin));
+        }
+        if (nf < K) {
+            collect = false;
+            return;
+        }
+        uint32_t kth = wave_kth_regs(kk, wave_umin(klo), wave_umax(khi), K);
+        kth = max(kth, __hip_atomic_load(&s.tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        wave_sync();
+        uint32_t m = 0;
+#pragma unroll
+        for (int q = 0; q < kPerL; q++) {
+            const bool keep = kk[q] >= kth;  // empty and -inf slots hold 0 < kth
+            const uint64_t bal = __ballot(keep);
+            if (keep) {
+                const uint32_t pos = m + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+                wkey[pos] = __float_as_uint(xr[q]);
+                widx[pos] = ii[q];
+            }
+            m += (uint32_t)__builtin_popcountll(bal);
+        }
+        wave_sync();
+        wn = __builtin_amdgcn_readfirstlane((int)m);
+        tau = key2f(kth);
+        xt = x_threshold(tau, invT);
+        if (g.lane == 0) atomicMax(&s.tau_key, kth);
+        compacted = true;
+    };
+    // kPF sweeps in flight per lane: the next group's loads are issued before this group is used
+    // (loads past the row return zeros, so they are issued unconditionally)
+    constexpr int kPF = 6;
+    {
+        f4 cur[kPF];
+#pragma unroll
+        for (int q = 0; q < kPF; q++) cur[q] = load4(lo + q * 256);
+        for (int gb = lo; gb < hi; gb += kPF * 256) {
+            // another wave may have raised the shared bound: use it too
+            const uint32_t ts = __hip_atomic_load(&s.tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            f4 nxt[kPF];
+#pragma unroll
+            for (int q = 0; q < kPF; q++) nxt[q] = load4(gb + (kPF + q) * 256);
+            if (ts > f2key(tau)) {
+                tau = key2f(ts);
+                xt = x_threshold(tau, invT);
+            }
+#pragma unroll
+            for (int q = 0; q < kPF; q++) {
+                const int base = gb + q * 256;
+                if (base >= hi || !collect) continue;  // (no early exits: they cost structurizer state)
+                const float xv[4] = {cur[q].x, cur[q].y, cur[q].z, cur[q].w};
+                M = __builtin_elementwise_maximum(M, __builtin_elementwise_maximum(xv[0], xv[1]));
+                M = __builtin_elementwise_maximum(M, __builtin_elementwise_maximum(xv[2], xv[3]));
+                int cnt = 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) cnt += __builtin_popcountll(__ballot(xv[j] >= xt));
+                if (wn + cnt > kCapW) {  // full: compact, then test again against the raised bound
+                    compact();
+                    cnt = 0;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) cnt += __builtin_popcountll(__ballot(xv[j] >= xt));
+                    if (wn + cnt > kCapW) collect = false;  // ties: the general kernel
+                }
+                if (cnt == 0 || !collect) continue;
+                const int i0 = base + 4 * g.lane;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const bool c = xv[j] >= xt;
+                    const uint64_t bal = __ballot(c);
+                    // position: the buffer fill plus the candidates in lower lanes
+                    const uint32_t pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bal, (uint32_t)wn));
+                    if (c) {
+                        wkey[pos] = __float_as_uint(xv[j]);
+                        widx[pos] = i0 + j;
+                    }
+                    wn += __builtin_popcountll(bal);
+                }
+                wn = __builtin_amdgcn_readfirstlane(wn);
+            }
+            collect = __builtin_amdgcn_readfirstlane((int)collect) != 0;
+            if (!collect) break;
+#pragma unroll
+            for (int q = 0; q < kPF; q++) cur[q] = nxt[q];
+        }
+    }
+    // the buffered entries as keys of their exact values, -inf values dropped
+    if (collect) {
+        wave_sync();
+        uint32_t kk[kPerL];
+        int32_t ii[kPerL];
+        bool fin[kPerL];
+#pragma unroll
+        for (int q = 0; q < kPerL; q++) {
+            const int j = g.lane + 64 * q;
+            ii[q] = widx[j];
+            const bool in = j < wn;
+            const float v = vexact(in ? ii[q] : lo, __uint_as_float(wkey[j]));
+            fin[q] = in && v > kNegInf;
+            kk[q] = f2key(v);
+        }
+        wave_sync();
+        uint32_t m = 0;
+#pragma unroll
+        for (int q = 0; q < kPerL; q++) {
+            const uint64_t bal = __ballot(fin[q]);
+            if (fin[q]) {
+                const uint32_t pos = m + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+                wkey[pos] = kk[q];
+                widx[pos] = ii[q];
+            }
+            m += (uint32_t)__builtin_popcountll(bal);
+        }
+        wave_sync();
+        wn = (int)m;
+    }
+    if (g.lane == 0) {
+        s.wcnt[g.wv] = collect ? wn : -1;
+        s.wcomp[g.wv] = compacted ? 1 : 0;
+    }
+    // NaN or fl(M * 1/T) = +inf: check the row exactly with the full transform (suppression, or a
+    // penalty, may have removed or lowered that value)
+    bool bad = false;
+    if (g.any(M != M || M * invT == kPosInf))
+        for_row(xrow, V, vec, g.t, X, [&](int, float v) { bad |= __builtin_amdgcn_class(v, 0x203); });
+    if (g.any(bad)) {
+        if (g.t == 0) a.out_ids[r] = VXS_ERR_NONFINITE;
+        return;
+    }
+    // The finite count is the buffered total unless some wave compacted, which takes more than k
+    // finite entries (a count of "many" decides top-k the same way).
+    bool all = true, comp = false;
+    uint32_t tot = 0;
+#pragma unroll
+    for (int w = 0; w < kWW; w++) {
+        all = all && s.wcnt[w] >= 0;
+        comp = comp || s.wcomp[w] != 0;
+        tot += (uint32_t)max(s.wcnt[w], 0);
+    }
+    if (!all) {
+        if (g.t == 0) a.out_ids[r] = kPendingId;
+        return;
+    }
+    const uint32_t cnt = comp ? (uint32_t)V : tot;
+    float* orow = a.out_logits ? a.out_logits + (int64_t)r * V : nullptr;
+    double* prow = a.out_probs ? a.out_probs + (int64_t)r * V : nullptr;
+    if (cnt == 0) {  // every entry -inf: the reference's draw returns the last id
+        if (g.t == 0) a.out_ids[r] = V - 1;
+        if (orow) for_row(xrow, V, vec, g.t, X, [&](int i, float x) { orow[i] = x; });
+        if (prow)
+            for (int i = g.t; i < V; i += kTW) prow[i] = __builtin_nan("");
+        return;
+    }
+    const bool topk_on = (uint32_t)K < cnt;
+    uint64_t* ckey = reinterpret_cast<uint64_t*>(s.ex.cp);  // (d, index) keys before the probabilities
+
+    // ---- wave 0: k-th largest of the four buffers, the maximum, the candidates
+    if (g.wv == 0) {
+        constexpr int kSl = kWW * kPerL;
+        uint32_t kk[kSl];
+        int32_t ii[kSl];
+        uint32_t klo = 0xffffffffu, khi = 0;
+#pragma unroll
+        for (int w = 0; w < kWW; w++) {
+            const int wc = s.wcnt[w];
+#pragma unroll
+            for (int q = 0; q < kPerL; q++) {
+                const int j = g.lane + 64 * q;
+                const bool in = j < wc;
+                kk[w * kPerL + q] = in ? s.wkey[w][j] : 0u;  // finite keys are > 0
+                ii[w * kPerL + q] = s.widx[w][j];
+                klo = in ? min(klo, s.wkey[w][j]) : klo;
+                khi = in ? max(khi, s.wkey[w][j]) : khi;
+            }
+        }
+        khi = wave_umax(khi);
+        const uint32_t kthkey = topk_on ? wave_kth_regs(kk, wave_umin(klo), khi, K) : 1u;
+        const float mx = key2f(khi);
+        int n = 0;
+#pragma unroll
+        for (int q = 0; q < kSl; q++) {
+            const bool keep = kk[q] >= kthkey;
+            const uint64_t bal = __ballot(keep);
+            const int pos = n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+            if (keep && pos < kCandW) {
+                const float v = key2f(kk[q]);
+                s.ex.cx[pos] = v;
+                s.ex.ci[pos] = ii[q];
+                ckey[pos] = ((uint64_t)f2key(v - mx) << 32) | (uint32_t)ii[q];
+            }
+            n += __builtin_popcountll(bal);
+        }
+        if (g.lane == 0) {
+            s.n = n;
+            s.kth_key = topk_on ? kthkey : 0u;
+            s.mx = mx;
+        }
+    }
+    __syncthreads();
+    const int n = s.n;
+    const float kth = topk_on ? key2f(s.kth_key) : kNegInf;
+    const float mx = s.mx;
+    if (n > kCandW) {  // ties beyond the exact-regime capacity
+        if (g.t == 0) a.out_ids[r] = kPendingId;
+        return;
+    }
+    if (orow) for_row(xrow, V, vec, g.t, X, [&](int i, float x) { orow[i] = x < kth ? kNegInf : x; });
+    if (prow)
+        for (int i = g.t; i < V; i += kTW) prow[i] = 0.0;
+
+    // ---- all waves: each candidate's position in index order and in (d, index) order
+    int io = 0, po = 0;
+    float cxt = 0.0f;
+    int32_t cit = 0;
+    if (g.t < n) {
+        const uint64_t kt = ckey[g.t];
+        cxt = s.ex.cx[g.t];
+        cit = s.ex.ci[g.t];
+#pragma unroll 8
+        for (int l = 0; l < n; l++) {
+            const uint64_t kl = ckey[l];
+            io += (uint32_t)kl < (uint32_t)kt ? 1 : 0;
+            po += kl < kt ? 1 : 0;
+        }
+    }
+    __syncthreads();
+    if (g.t < n) {
+        s.ex.cx[io] = cxt;
+        s.ex.ci[io] = cit;
+        s.ex.cs[po] = (int16_t)io;
+    }
+    __syncthreads();
+    if (g.wv != 0) return;
+
+    // ---- wave 0: the reference's fp64 arithmetic on the candidates in index order
+    double* cp = s.ex.cp;
+    for (int j = g.lane; j < n; j += 64) cp[j] = exp((double)(s.ex.cx[j] - mx));  // Sampler.cs:57
+    wave_sync();
+    const double sum = seq_sum(cp, n);  // sequential in index order                   :58
+    for (int j = g.lane; j < n; j += 64) cp[j] = cp[j] / sum;  //                         :60
+    wave_sync();
+    if (P.top_p < 1.0f) {  //                                                          :62-75
+        bool ok = true;
+        for (int q = g.lane; q < n - 1; q += 64) {
+            const int a0 = s.ex.cs[q], b0 = s.ex.cs[q + 1];
+            const double pa = cp[a0], pb = cp[b0];
+            ok = ok && (pa < pb || (pa == pb && a0 < b0));
+        }
+        if (__ballot(!ok)) {  // rank by (p, index) directly
+            int rk[kCandW / 64];
+#pragma unroll
+            for (int k = 0; k < kCandW / 64; k++) {
+                const int j = g.lane + 64 * k;
+                rk[k] = j < n ? seq_rank(cp, n, j) : 0;
+            }
+            wave_sync();
+#pragma unroll
+            for (int k = 0; k < kCandW / 64; k++) {
+                const int j = g.lane + 64 * k;
+                if (j < n) s.ex.cs[rk[k]] = (int16_t)j;
+            }
+            wave_sync();
+        }
+        // the last sorted position is never removed (the reference's loop runs j < n - 1)
+        const int nrem = seq_topp_cut(cp, s.ex.cs, n, (double)(1.0f - P.top_p));
+        for (int q = g.lane; q < nrem; q += 64) cp[s.ex.cs[q]] = 0.0;
+        wave_sync();
+        const double s2 = seq_sum(cp, n);
+        for (int j = g.lane; j < n; j += 64) cp[j] = cp[j] / s2;
+        wave_sync();
+    }
+    const double u = a.u ? a.u[r] : 0.0;
+    const int pick = seq_draw(cp, s.ex.ci, n, u);  // inverse-CDF draw in index order     :77-87
+    if (g.lane == 0) a.out_ids[r] = pick;
+    if (prow)
+        for (int j = g.lane; j < n; j += 64) prow[s.ex.ci[j]] = cp[j];
+}
+
 }  // namespace
 
 hipError_t launch_sample_wide(const SampleArgs& a, hipStream_t stream) {
     if (a.rows <= 0) return hipSuccess;
     if (a.vocab <= 0 || a.vocab > kWideMaxVocab) return hipErrorNotSupported;
     const int vec = (a.ld % 4 == 0) && (((uintptr_t)a.logits & 15u) == 0) ? 1 : 0;
-    const size_t dyn = sizeof(uint32_t) * (size_t)((a.vocab + 31) / 32);
+    const size_t dyn = sizeof(uint32_t) * (size_t)((a.vocab + 31) / 32 + kBmPad);
+    // the ordered kernel first; the general kernel serves every other row and the rows it left
+    hipLaunchKernelGGL(sample_wide_ordered_kernel, dim3(a.rows), dim3(kTW), dyn, stream, a, vec);
     hipLaunchKernelGGL(sample_wide_kernel, dim3(a.rows), dim3(kTW), dyn, stream, a, vec);
     return hipGetLastError();
 }
