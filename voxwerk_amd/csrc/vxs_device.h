@@ -223,6 +223,16 @@ __device__ __forceinline__ float key2f(uint32_t k) {
 // They run redundantly in every thread on LDS broadcast reads; LDS is read 8 entries at a time so
 // one read latency covers eight steps, and the steps are branch-free.
 
+// A zero the compiler cannot prove wave-uniform. Indexing the LDS reads of a sequential loop with
+// it keeps the loop's running counts in vector registers: otherwise every compare result of a
+// broadcast value is moved to a scalar register (a read-first-lane and a dependent scalar add per
+// step, several times slower than the vector count).
+__device__ __forceinline__ int lane_zero() {
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return z;
+}
+
 // Left-to-right double sum of x[0..n) (the reference's sequential Sum).
 __device__ __forceinline__ double seq_sum(const double* x, int n) {
     double s = 0.0;
@@ -244,12 +254,16 @@ __device__ __forceinline__ double seq_sum(const double* x, int n) {
 // position with !(cum <= thr) equals the number of prefixes with cum <= thr, counted off the
 // critical path of the additions; the scan stops after the deciding batch.
 __device__ __forceinline__ int seq_topp_cut(const double* p, const int16_t* order, int n, double thr) {
+    const int z = lane_zero();
     double cum = 0.0;
     int nrem = 0;
     for (int s0 = 0; s0 < n - 1 && nrem == s0; s0 += 8) {
         double pb[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) pb[k] = s0 + k < n - 1 ? p[order[s0 + k]] : 0.0;
+        for (int k = 0; k < 8; k++) {  // clamped indices: the reads are unconditional and overlap
+            const double pk = p[order[min(s0 + k, n - 1) + z]];
+            pb[k] = s0 + k < n - 1 ? pk : 0.0;
+        }
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             cum += pb[k];
@@ -265,6 +279,7 @@ __device__ __forceinline__ int seq_topp_cut(const double* p, const int16_t* orde
 // unchanged, and it never decreases until it turns NaN, so the first crossing is the number of
 // prefixes <= u, provided that is below the first NaN prefix.
 __device__ __forceinline__ int seq_draw(const double* p, const int32_t* id, int n, double u) {
+    const int z = lane_zero();
     double acc = 0.0;
     int below_u = 0, nan_prefixes = 0, lastj = -1, scanned = 0;
     for (int j0 = 0; j0 < n && below_u == j0 && nan_prefixes == 0; j0 += 8) {
@@ -272,7 +287,8 @@ __device__ __forceinline__ int seq_draw(const double* p, const int32_t* id, int 
         double pb[8];
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            const double pj = j0 + k < n ? p[j0 + k] : 0.0;
+            const double pk = p[min(j0 + k, n - 1) + z];  // clamped: unconditional reads
+            const double pj = j0 + k < n ? pk : 0.0;
             const bool take = !(pj <= 0.0);
             pb[k] = take ? pj : 0.0;
             lastj = take ? j0 + k : lastj;
@@ -292,6 +308,90 @@ __device__ __forceinline__ int seq_draw(const double* p, const int32_t* id, int 
     if (nan_prefixes > 0)
         for (int j = 0; j < n; j++) lastj = !(p[j] <= 0.0) ? j : lastj;
     return lastj >= 0 ? id[lastj] : 0;
+}
+
+// ---- one-wave forms of the top-p cut and the draw: the dependent loop only adds and records
+// each prefix (lane 0 stores it to LDS scratch, 8 at a time); the compares then run lane-parallel
+// over the recorded prefixes. Same results as seq_topp_cut and seq_draw.
+
+// seq_topp_cut by one wave, on the probabilities already gathered into sorted order
+// (ps[s] = p[order[s]]); scr holds n - 1 doubles of LDS.
+__device__ __forceinline__ int wave_topp_cut(const double* ps, int n, double thr, double* scr, int lane) {
+    const int m = n - 1;  // the positions the reference may remove
+    const int z = lane_zero();
+    double cum = 0.0;
+    int end = 0;  // prefixes recorded
+    bool over = false;
+    for (; end + 8 <= m && !over; end += 8) {
+        double c[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            cum += ps[end + k + z];
+            c[k] = cum;
+        }
+        if (lane == 0)
+#pragma unroll
+            for (int k = 0; k < 8; k++) scr[end + k] = c[k];
+        over = !(cum <= thr);  // the deciding prefix is recorded: the rest exceed thr (or are NaN)
+    }
+    for (; end < m && !over; end++) {
+        cum += ps[end + z];
+        if (lane == 0) scr[end] = cum;
+        over = !(cum <= thr);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint32_t cnt = 0;
+    for (int q = lane; q < end; q += 64) cnt += scr[q] <= thr ? 1u : 0u;
+    return (int)wave_sum(cnt);
+}
+
+// seq_draw by one wave; scr holds n doubles of LDS. Skipped entries (p <= 0) hold +0 here (the
+// probabilities are exp(d) / sum >= +0, removed ones +0), so adding them leaves the running sum
+// unchanged and the loop adds every entry.
+__device__ __forceinline__ int wave_draw(const double* p, const int32_t* id, int n, double u, double* scr,
+                                         int lane) {
+    const int z = lane_zero();
+    double acc = 0.0;
+    int end = 0;
+    bool stop = false;  // a prefix above u (or NaN) is recorded
+    for (; end + 8 <= n && !stop; end += 8) {
+        double c[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            acc += p[end + k + z];
+            c[k] = acc;
+        }
+        if (lane == 0)
+#pragma unroll
+            for (int k = 0; k < 8; k++) scr[end + k] = c[k];
+        stop = !(acc <= u);
+    }
+    for (; end < n && !stop; end++) {
+        acc += p[end + z];
+        if (lane == 0) scr[end] = acc;
+        stop = !(acc <= u);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // the running sum never decreases until it turns NaN: the first crossing is the number of
+    // prefixes <= u, provided that is below the first NaN prefix
+    uint32_t below = 0, first_nan = (uint32_t)n;
+    for (int q = lane; q < end; q += 64) {
+        const double a = scr[q];
+        below += a <= u ? 1u : 0u;
+        if (a != a) first_nan = min(first_nan, (uint32_t)q);
+    }
+    below = wave_sum(below);
+    first_nan = wave_umin(first_nan);
+    if (below < first_nan) return id[below];
+    // no crossing: the last entry with p > 0 or NaN (0 when none)
+    int last = -1;
+    for (int q = lane; q < n; q += 64) last = !(p[q] <= 0.0) ? q : last;
+    last = (int)wave_umax((uint32_t)(last + 1)) - 1;
+    return last >= 0 ? id[last] : 0;
 }
 
 // Stable ascending (p, index) rank of entry j among p[0..n).

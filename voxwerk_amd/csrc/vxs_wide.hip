@@ -37,6 +37,7 @@ constexpr int kCapW = 512;        // candidate buffer entries per wave
 constexpr int kPerL = kCapW / 64;  // ... per lane
 constexpr int kKMax = 256;        // largest top-k of the streaming path
 constexpr int kCandW = 256;       // exact-regime capacity
+constexpr int kUnion = 1536;      // ordered kernel: the four buffers' entries after pass A, at most
 constexpr int kRB = 256;          // radix buckets (8-bit digits)
 // zero words after the history bitmap: a sweep's lanes past the row end (up to 255 entries) read
 // bitmap words within the allocation
@@ -52,7 +53,7 @@ struct WideSmem {
     // within 40 KB of LDS, four workgroups (16 waves) per CU.
     union {
         union {
-            uint32_t hcnt[kRB];
+            alignas(16) uint32_t hcnt[kRB];
             double hmass[kRB];
         } h;
         struct {
@@ -65,6 +66,7 @@ struct WideSmem {
     uint64_t slot[4][kWW];
     int32_t wcnt[kWW];  // per-wave candidate counts after pass A (-1: the wave's buffer overflowed)
     int32_t wcomp[kWW]; // per-wave: the buffer was compacted at least once (ordered kernel)
+    int32_t wslot[kWW]; // per-wave: the wave's SIMD matches the workgroup's slot on its CU (ordered kernel)
     uint32_t tau_key;   // the largest k-th largest any wave has found so far (a shared lower bound)
     uint32_t kth_key;   // ordered kernel: the row's k-th largest (0 without top-k) ...
     float mx;           // ... and its maximum
@@ -198,6 +200,78 @@ __device__ __forceinline__ uint32_t wave_kth_regs(const uint32_t (&kk)[N], uint3
         else hi = mid - 1;
     }
     return lo;
+}
+
+// A key K with at least k of the register-held keys >= K and at most k + slack of them (or the
+// exact k-th largest, where ties leave no such K): a bisection over [lo, hi] that stops as soon
+// as the count falls in that window. Any such K is a lower bound of the k-th largest.
+template <int N>
+__device__ __forceinline__ uint32_t wave_bound_regs(const uint32_t (&kk)[N], uint32_t lo, uint32_t hi, int k,
+                                                    int slack) {
+#pragma unroll 1
+    while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo + 1) >> 1);
+        int c = 0;
+#pragma unroll
+        for (int q = 0; q < N; q++) c += __builtin_popcountll(__ballot(kk[q] >= mid));
+        if (c >= k) {
+            lo = mid;
+            if (c <= k + slack) break;
+        } else {
+            hi = mid - 1;
+        }
+    }
+    return lo;
+}
+
+// The exact k-th largest (with multiplicity) of the keys a wave holds in registers (0 = empty
+// slot, at least k valid in [klo, khi]), by a radix select in LDS: 8-bit digits from the highest
+// bit in which the valid keys differ. hist: 256 words of LDS used by this wave alone.
+template <int N>
+__device__ __forceinline__ uint32_t wave_kth_radix(const uint32_t (&kk)[N], uint32_t klo, uint32_t khi, int k,
+                                                   uint32_t* hist, int lane) {
+    if (klo == khi) return khi;
+    const int top = 31 - __clz(klo ^ khi);                        // highest bit that differs
+    uint32_t mask = top == 31 ? 0u : ~((2u << top) - 1u);          // the bits every valid key shares ...
+    uint32_t prefix = khi & mask;                                  // ... and their value
+    int need = k;
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+#pragma unroll 1
+    for (int lo_bit = top - 7;; lo_bit -= 8) {
+        const int sh = lo_bit > 0 ? lo_bit : 0;
+        const uint32_t dmask = (lo_bit >= 0 ? 0xffu : (0xffu >> -lo_bit));
+        reinterpret_cast<u4*>(hist)[lane] = u4{0u, 0u, 0u, 0u};
+        wave_sync();
+#pragma unroll
+        for (int q = 0; q < N; q++)
+            if (kk[q] != 0u && (kk[q] & mask) == prefix) atomicAdd(&hist[(kk[q] >> sh) & dmask], 1u);
+        wave_sync();
+        // lane l takes bins 255 - 4l down to 252 - 4l: the counts in descending digit order
+        const u4 h4 = reinterpret_cast<const u4*>(hist)[63 - lane];
+        const uint32_t c[4] = {h4.w, h4.z, h4.y, h4.x};
+        const uint32_t tot = c[0] + c[1] + c[2] + c[3];
+        const uint32_t incl = wave_incl_sum(tot);
+        uint32_t run = incl - tot;  // entries in higher digits than this lane's
+        int digit = -1;
+        uint32_t above = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            if (digit < 0 && run < (uint32_t)need && run + c[b] >= (uint32_t)need) {
+                digit = 255 - 4 * lane - b;
+                above = run;
+            }
+            run += c[b];
+        }
+        const uint64_t who = __ballot(digit >= 0);
+        const int src = __builtin_ctzll(who);
+        const uint32_t d = (uint32_t)__builtin_amdgcn_readlane(digit, src);
+        need -= (int)__builtin_amdgcn_readlane(above, src);
+        prefix |= d << sh;
+        mask |= dmask << sh;
+        wave_sync();
+        if (sh == 0) break;
+    }
+    return prefix;
 }
 
 // k-th largest (1-based, with multiplicity) of a wave's n >= k buffered keys; wave-local.
@@ -907,8 +981,8 @@ __device__ __forceinline__ float x_threshold(float tau, float invT) {
 // waves). Sweeps that suppression or the range end touch apply the full transform per entry. NaN
 // reaches the NaN-propagating maximum M of the raw values; fl(M * 1/T) = +inf sends the row
 // through an exact check with the full transform (the penalty may have lowered that value).
-// Tail: wave 0 finds the k-th largest of the four buffers by bisection and extracts the
-// candidates; all waves rank them by index and by (d, index), d = v - max; wave 0 runs the
+// Tail: one wave finds the k-th largest of the four buffers by a radix select and extracts the
+// candidates; all waves rank them by index and by (d, index), d = v - max; that wave runs the
 // reference's sequential fp64 arithmetic (S6-S8, Sampler.cs:51-87). The (d, index) order is the
 // reference's (p, index) order whenever each adjacent pair is in (p, index) order (p = exp(d) / sum
 // never decreases with d for a monotone exp); otherwise the candidates are ranked by p directly.
@@ -930,6 +1004,13 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
     const float* __restrict__ xrow = a.logits + (int64_t)r * a.ld;
     const float invT = row_inv_temp(P);
     const int K = P.top_k;
+    {
+        // HW_ID: SIMD_ID in bits 5:4, the workgroup's slot on its CU in bits 19:16. The wave whose
+        // SIMD equals the slot runs this row's sequential tail, so the tails of the workgroups
+        // sharing a CU land on different SIMDs (checked below: exactly one such wave, else wave 0).
+        const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+        if (g.lane == 0) s.wslot[g.wv] = ((hw >> 4) & 3u) == ((hw >> 16) & 3u) ? 1 : 0;
+    }
 
     RowX X;
     X.bm = nullptr;
@@ -997,7 +1078,8 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
             collect = false;
             return;
         }
-        uint32_t kth = wave_kth_regs(kk, wave_umin(klo), wave_umax(khi), K);
+        // a lower bound of the row's k-th largest that keeps at most k + 32 entries (untied)
+        uint32_t kth = wave_bound_regs(kk, wave_umin(klo), wave_umax(khi), K, 32);
         kth = max(kth, __hip_atomic_load(&s.tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
         wave_sync();
         uint32_t m = 0;
@@ -1077,9 +1159,12 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
             for (int q = 0; q < kPF; q++) cur[q] = nxt[q];
         }
     }
-    // the buffered entries as keys of their exact values, -inf values dropped
+    // the buffered entries as keys of their exact values, keeping the finite ones at or above the
+    // shared bound (a fuller buffer is compacted first, so that the four fit the union's capacity)
+    if (collect && wn > kUnion / kWW) compact();
     if (collect) {
         wave_sync();
+        const uint32_t ts = __hip_atomic_load(&s.tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         uint32_t kk[kPerL];
         int32_t ii[kPerL];
         bool fin[kPerL];
@@ -1089,8 +1174,8 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
             ii[q] = widx[j];
             const bool in = j < wn;
             const float v = vexact(in ? ii[q] : lo, __uint_as_float(wkey[j]));
-            fin[q] = in && v > kNegInf;
             kk[q] = f2key(v);
+            fin[q] = in && v > kNegInf && kk[q] >= ts;
         }
         wave_sync();
         uint32_t m = 0;
@@ -1131,7 +1216,7 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
         comp = comp || s.wcomp[w] != 0;
         tot += (uint32_t)max(s.wcnt[w], 0);
     }
-    if (!all) {
+    if (!all || tot > (uint32_t)kUnion) {  // a wave stopped collecting, or ties fill the buffers
         if (g.t == 0) a.out_ids[r] = kPendingId;
         return;
     }
@@ -1148,27 +1233,37 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
     const bool topk_on = (uint32_t)K < cnt;
     uint64_t* ckey = reinterpret_cast<uint64_t*>(s.ex.cp);  // (d, index) keys before the probabilities
 
-    // ---- wave 0: k-th largest of the four buffers, the maximum, the candidates
-    if (g.wv == 0) {
-        constexpr int kSl = kWW * kPerL;
+    bool worker = g.wv == 0;  // the wave that runs the sequential tail
+    {
+        int nw = 0;
+#pragma unroll
+        for (int w = 0; w < kWW; w++) nw += s.wslot[w];
+        if (nw == 1) worker = s.wslot[g.wv] != 0;
+    }
+    // ---- the worker wave: k-th largest of the four buffers, the maximum, the candidates
+    if (worker) {
+        // the four buffers, concatenated in order, kSl entries per lane (tot <= kUnion)
+        constexpr int kSl = kUnion / 64;
         uint32_t kk[kSl];
         int32_t ii[kSl];
         uint32_t klo = 0xffffffffu, khi = 0;
+        const int b1 = s.wcnt[0], b2 = b1 + s.wcnt[1], b3 = b2 + s.wcnt[2];
+        const uint32_t* fkey = &s.wkey[0][0];
+        const int32_t* fidx = &s.widx[0][0];
 #pragma unroll
-        for (int w = 0; w < kWW; w++) {
-            const int wc = s.wcnt[w];
-#pragma unroll
-            for (int q = 0; q < kPerL; q++) {
-                const int j = g.lane + 64 * q;
-                const bool in = j < wc;
-                kk[w * kPerL + q] = in ? s.wkey[w][j] : 0u;  // finite keys are > 0
-                ii[w * kPerL + q] = s.widx[w][j];
-                klo = in ? min(klo, s.wkey[w][j]) : klo;
-                khi = in ? max(khi, s.wkey[w][j]) : khi;
-            }
+        for (int q = 0; q < kSl; q++) {
+            const int e = g.lane + 64 * q;
+            const bool in = e < (int)tot;
+            const int j = e < b1 ? e : e < b2 ? kCapW + e - b1 : e < b3 ? 2 * kCapW + e - b2 : 3 * kCapW + e - b3;
+            const int jj = in ? j : 0;  // unconditional reads
+            const uint32_t key = fkey[jj];
+            ii[q] = fidx[jj];
+            kk[q] = in ? key : 0u;  // finite keys are > 0
+            klo = in ? min(klo, key) : klo;
+            khi = in ? max(khi, key) : khi;
         }
         khi = wave_umax(khi);
-        const uint32_t kthkey = topk_on ? wave_kth_regs(kk, wave_umin(klo), khi, K) : 1u;
+        const uint32_t kthkey = topk_on ? wave_kth_radix(kk, wave_umin(klo), khi, K, s.h.hcnt, g.lane) : 1u;
         const float mx = key2f(khi);
         int n = 0;
 #pragma unroll
@@ -1225,10 +1320,11 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
         s.ex.cs[po] = (int16_t)io;
     }
     __syncthreads();
-    if (g.wv != 0) return;
+    if (!worker) return;
 
-    // ---- wave 0: the reference's fp64 arithmetic on the candidates in index order
+    // ---- the worker wave: the reference's fp64 arithmetic on the candidates in index order
     double* cp = s.ex.cp;
+    double* scr = reinterpret_cast<double*>(&s.wkey[0][0]);  // the prefixes of the cut and the draw
     for (int j = g.lane; j < n; j += 64) cp[j] = exp((double)(s.ex.cx[j] - mx));  // Sampler.cs:57
     wave_sync();
     const double sum = seq_sum(cp, n);  // sequential in index order                   :58
@@ -1257,7 +1353,10 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
             wave_sync();
         }
         // the last sorted position is never removed (the reference's loop runs j < n - 1)
-        const int nrem = seq_topp_cut(cp, s.ex.cs, n, (double)(1.0f - P.top_p));
+        double* ps = reinterpret_cast<double*>(&s.widx[0][0]);  // p in (p, index) order
+        for (int q = g.lane; q < n; q += 64) ps[q] = cp[s.ex.cs[q]];
+        wave_sync();
+        const int nrem = wave_topp_cut(ps, n, (double)(1.0f - P.top_p), scr, g.lane);
         for (int q = g.lane; q < nrem; q += 64) cp[s.ex.cs[q]] = 0.0;
         wave_sync();
         const double s2 = seq_sum(cp, n);
@@ -1265,7 +1364,7 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
         wave_sync();
     }
     const double u = a.u ? a.u[r] : 0.0;
-    const int pick = seq_draw(cp, s.ex.ci, n, u);  // inverse-CDF draw in index order     :77-87
+    const int pick = wave_draw(cp, s.ex.ci, n, u, scr, g.lane);  // inverse-CDF draw in index order :77-87
     if (g.lane == 0) a.out_ids[r] = pick;
     if (prow)
         for (int j = g.lane; j < n; j += 64) prow[s.ex.ci[j]] = cp[j];
