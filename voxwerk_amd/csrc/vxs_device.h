@@ -219,6 +219,28 @@ __device__ __forceinline__ float key2f(uint32_t k) {
     return __uint_as_float(u);
 }
 
+// A key K with at least k of the register-held keys >= K and at most k + slack of them (or the
+// exact k-th largest, where ties leave no such K): a bisection over [lo, hi] that stops as soon
+// as the count falls in that window. Any such K is a lower bound of the k-th largest.
+template <int N>
+__device__ __forceinline__ uint32_t wave_bound_regs(const uint32_t (&kk)[N], uint32_t lo, uint32_t hi, int k,
+                                                    int slack) {
+#pragma unroll 1
+    while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo + 1) >> 1);
+        int c = 0;
+#pragma unroll
+        for (int q = 0; q < N; q++) c += __builtin_popcountll(__ballot(kk[q] >= mid));
+        if (c >= k) {
+            lo = mid;
+            if (c <= k + slack) break;
+        } else {
+            hi = mid - 1;
+        }
+    }
+    return lo;
+}
+
 // ---- sequential phases of the exact regime (the reference's fp64 loops, Sampler.cs:58-87) ----
 // They run redundantly in every thread on LDS broadcast reads; LDS is read 8 entries at a time so
 // one read latency covers eight steps, and the steps are branch-free.

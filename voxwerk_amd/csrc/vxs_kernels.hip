@@ -76,7 +76,8 @@ enum Site : int {
     kSiteRefine,
     kSiteRefine2,
     kSiteRefine3,
-    kSiteComp0,  // + NC
+    kSiteTk0,    // + 2
+    kSiteComp0 = kSiteTk0 + 2,  // + NC
     kSiteChunk0 = kSiteComp0 + 8,  // + NC
     kSiteNScan0 = kSiteChunk0 + 8,  // + NC + 1
     kSites = kSiteNScan0 + 9,
@@ -185,6 +186,7 @@ struct Ctl {
     double S, T, below;
     int32_t bstar;
     double kept[8];
+    float tk_kth;  // top-k: the k-th largest value
 };
 
 template <int NC>
@@ -193,6 +195,7 @@ struct RowSmem {
     uint32_t bm[C::BMW];
     union {
         float xs[C::VMAX];  // staged row for the penalty
+        float tmax[kT];     // top-k: the threads' largest values
         struct {
             double hist[kNB];
             uint32_t lkey[kLMax];
@@ -206,7 +209,10 @@ struct RowSmem {
             float cx[kCandMax];
             int32_t ci[kCandMax];
             double cp[kCandMax];
+            double ps[kCandMax];   // p in (p, index) order, for the top-p cut
+            double pre[kCandMax];  // the running sums of the cut and of the draw
             int16_t cs[kCandMax];
+            int32_t nrem;
         } ex;
     } u;
     struct {
@@ -720,7 +726,92 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
 
     // ---- S5: top-k (ties at the k-th value are kept)
     const int K = P.top_k;
-    if (K > 0 && K < V && (uint32_t)K < cnt) {
+    bool cands = false;  // the exact-regime arrays already hold the candidates in index order
+    int ncand = 0;
+    if (K > 0 && K < V && (uint32_t)K < cnt && K <= kCandMax) {
+        // A lower bound T of the k-th largest: at least K of the 256 thread maxima (a subset of
+        // the row) are >= T, and at most K + 32 unless ties force more. When the entries >= T
+        // fit the exact-regime capacity they are the candidates: all entries >= the k-th largest
+        // are among them, so their own k-th largest is the row's.
+        float tm = kNegInf;
+#pragma unroll
+        for (int e = 0; e < NE; e++) tm = fmaxf(tm, v[e]);
+        sm.u.tmax[g.t] = tm;
+        g.sync();
+        uint32_t mk[kT / 64];
+        uint32_t mlo = 0xffffffffu, mhi = 0;
+#pragma unroll
+        for (int q = 0; q < kT / 64; q++) {
+            mk[q] = f2key(sm.u.tmax[g.lane + 64 * q]);
+            mlo = min(mlo, mk[q]);
+            mhi = max(mhi, mk[q]);
+        }
+        const float Tb = key2f(wave_bound_regs(mk, wave_umin(mlo), wave_umax(mhi), K, 32));
+        // the entries >= Tb in index order: 16-bit counts per sweep, four sweeps per scan
+        auto& ex = sm.u.ex;
+        uint32_t tot = 0;
+        uint64_t excl[(NC + 3) / 4], totals[(NC + 3) / 4];
+#pragma unroll
+        for (int h = 0; h < (NC + 3) / 4; h++) {
+            uint64_t mine = 0;
+#pragma unroll
+            for (int c = 4 * h; c < NC && c < 4 * h + 4; c++) {
+                uint32_t m = 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) m += v[c * 4 + j] >= Tb ? 1u : 0u;
+                mine |= (uint64_t)m << (16 * (c - 4 * h));
+            }
+            excl[h] = g.excl_scan(mine, kSiteTk0 + h, totals[h]);
+#pragma unroll
+            for (int c = 4 * h; c < NC && c < 4 * h + 4; c++) tot += (uint32_t)((totals[h] >> (16 * (c - 4 * h))) & 0xffffu);
+        }
+        if (tot <= (uint32_t)kCandMax) {
+            uint32_t base = 0;
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const int h = c / 4, f = 16 * (c % 4);
+                uint32_t off = base + (uint32_t)((excl[h] >> f) & 0xffffu);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int e = c * 4 + j;
+                    if (v[e] >= Tb) {
+                        ex.cx[off] = v[e];
+                        ex.ci[off] = eidx(e);
+                        off++;
+                    }
+                }
+                base += (uint32_t)((totals[h] >> f) & 0xffffu);
+            }
+            g.sync();
+            // the k-th largest with multiplicity: #{> x} < K <= #{>= x}
+            const int n = (int)tot;
+            if (g.t < n) {
+                const float x = ex.cx[g.t];
+                int gt = 0, ge = 0;
+#pragma unroll 8
+                for (int l = 0; l < n; l++) {
+                    const float y = ex.cx[l];
+                    gt += y > x ? 1 : 0;
+                    ge += y >= x ? 1 : 0;
+                }
+                if (gt < K && K <= ge) sm.ctl.tk_kth = x;
+            }
+            g.sync();
+            const float kth = sm.ctl.tk_kth;
+            if (g.t < n && ex.cx[g.t] < kth) ex.cx[g.t] = kNegInf;  // masked: probability 0
+            uint32_t c2 = 0;
+#pragma unroll
+            for (int e = 0; e < NE; e++) {
+                if (v[e] < kth) v[e] = kNegInf;
+                c2 += (uint32_t)__builtin_popcountll(__ballot(v[e] != kNegInf));
+            }
+            cnt = g.wsum_u(c2, kSiteCnt2);  // its barrier also orders the masking above
+            mn = kth;
+            cands = true;
+            ncand = n;
+        }
+    }
+    if (!cands && K > 0 && K < V && (uint32_t)K < cnt) {
         for (int b = g.t; b < kNB; b += kT) sm.u.sel.hist[b] = 0.0;
         uint64_t act = 0;
         float fmn = kPosInf;  // smallest finite value
@@ -769,8 +860,10 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
     if (cnt <= (uint32_t)kCandMax) {
         // ================= exact regime: the reference's sequential fp64 arithmetic =================
         auto& ex = sm.u.ex;
-        g.sync();
-        if constexpr (NC <= 4) {
+        if (cands) {
+            // the top-k candidates, in index order (those below the k-th largest hold -inf)
+        } else if constexpr (NC <= 4) {
+            g.sync();
             // one scan for every sweep: 16-bit counts per sweep (at most kCandMax candidates)
             uint64_t mine = 0;
 #pragma unroll
@@ -798,6 +891,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
                 base += (uint32_t)((total >> (16 * c)) & 0xffffu);
             }
         } else {
+            g.sync();
             uint32_t base = 0;
 #pragma unroll
             for (int c = 0; c < NC; c++) {
@@ -825,7 +919,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
         g.sync();
         // Parallel phases stride the candidates over the workgroup; sequential phases run
         // redundantly in every thread on LDS broadcast reads, so each yields a uniform value.
-        const int n = (int)cnt;
+        const int n = cands ? ncand : (int)cnt;
         for (int j = g.t; j < n; j += kT) ex.cp[j] = exp((double)(ex.cx[j] - m));  // Sampler.cs:57
         g.sync();
         double sum = seq_sum(ex.cp, n);  // sequential in index order                      :58
@@ -839,9 +933,16 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
             const double thr = (double)(1.0f - P.top_p);
             // The largest (p, index) entry is the reference's last sorted position, which its
             // loop (j < n - 1) never visits; masked entries sort first with p = 0 and change
-            // nothing. The scan only reads; the removed prefix is zeroed after a barrier.
-            const int nrem = seq_topp_cut(ex.cp, ex.cs, n, thr);
+            // nothing. Wave 0 runs the cut on p gathered into sorted order; the removed prefix is
+            // zeroed after a barrier.
+            for (int q = g.t; q < n; q += kT) ex.ps[q] = ex.cp[ex.cs[q]];
             g.sync();
+            if (g.wv == 0) {
+                const int nr = wave_topp_cut(ex.ps, n, thr, ex.pre, g.lane);
+                if (g.lane == 0) ex.nrem = nr;
+            }
+            g.sync();
+            const int nrem = ex.nrem;
             for (int s = g.t; s < nrem; s += kT) ex.cp[ex.cs[s]] = 0.0;
             g.sync();
             double s2 = seq_sum(ex.cp, n);  // probs.Sum(), sequential
@@ -849,8 +950,10 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
             for (int j = g.t; j < n; j += kT) ex.cp[j] = ex.cp[j] / s2;
             g.sync();
         }
-        const int pick = seq_draw(ex.cp, ex.ci, n, u);  // inverse-CDF draw in index order   :77-87
-        if (g.t == 0) a.out_ids[r] = pick;
+        if (g.wv == 0) {  // inverse-CDF draw in index order                              :77-87
+            const int pick = wave_draw(ex.cp, ex.ci, n, u, ex.pre, g.lane);
+            if (g.lane == 0) a.out_ids[r] = pick;
+        }
         if (prow)
             for (int j = g.t; j < n; j += kT) prow[ex.ci[j]] = ex.cp[j];
         return;

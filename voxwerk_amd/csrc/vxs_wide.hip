@@ -202,28 +202,6 @@ __device__ __forceinline__ uint32_t wave_kth_regs(const uint32_t (&kk)[N], uint3
     return lo;
 }
 
-// A key K with at least k of the register-held keys >= K and at most k + slack of them (or the
-// exact k-th largest, where ties leave no such K): a bisection over [lo, hi] that stops as soon
-// as the count falls in that window. Any such K is a lower bound of the k-th largest.
-template <int N>
-__device__ __forceinline__ uint32_t wave_bound_regs(const uint32_t (&kk)[N], uint32_t lo, uint32_t hi, int k,
-                                                    int slack) {
-#pragma unroll 1
-    while (lo < hi) {
-        const uint32_t mid = lo + ((hi - lo + 1) >> 1);
-        int c = 0;
-#pragma unroll
-        for (int q = 0; q < N; q++) c += __builtin_popcountll(__ballot(kk[q] >= mid));
-        if (c >= k) {
-            lo = mid;
-            if (c <= k + slack) break;
-        } else {
-            hi = mid - 1;
-        }
-    }
-    return lo;
-}
-
 // The exact k-th largest (with multiplicity) of the keys a wave holds in registers (0 = empty
 // slot, at least k valid in [klo, khi]), by a radix select in LDS: 8-bit digits from the highest
 // bit in which the valid keys differ. hist: 256 words of LDS used by this wave alone.
