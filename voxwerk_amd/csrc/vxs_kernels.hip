@@ -76,8 +76,8 @@ enum Site : int {
     kSiteRefine,
     kSiteRefine2,
     kSiteRefine3,
-    kSiteTk0,    // + 2
-    kSiteComp0 = kSiteTk0 + 2,  // + NC
+    kSiteTk0,    // + 3
+    kSiteComp0 = kSiteTk0 + 3,  // + NC
     kSiteChunk0 = kSiteComp0 + 8,  // + NC
     kSiteNScan0 = kSiteChunk0 + 8,  // + NC + 1
     kSites = kSiteNScan0 + 9,
@@ -186,7 +186,8 @@ struct Ctl {
     double S, T, below;
     int32_t bstar;
     double kept[8];
-    float tk_kth;  // top-k: the k-th largest value
+    float tk_kth;  // top-k: the k-th largest value ...
+    int32_t tk_cnt;  // ... and the count of entries at or above it
 };
 
 template <int NC>
@@ -578,7 +579,17 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
 #pragma unroll
         for (int k = 0; k < HP; k++)
             if (h0 + g.t + k * kT < h1) own(pre[k]);
-        for (int h = h0 + g.t + HP * kT; h < h1; h += kT) own(a.hist_ids[h]);
+        for (int hb = h0 + HP * kT; hb < h1; hb += 4 * kT) {  // the rest, four ids per thread in flight
+            int id[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int h = hb + k * kT + g.t;
+                id[k] = h < h1 ? a.hist_ids[h] : 0;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                if (hb + k * kT + g.t < h1) own(id[k]);
+        }
         if (g.any(bad, kSiteErr)) {
             if (g.t == 0) a.out_ids[r] = VXS_ERR_ID_OUT_OF_RANGE;
             return;
@@ -794,18 +805,19 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
                     gt += y > x ? 1 : 0;
                     ge += y >= x ? 1 : 0;
                 }
-                if (gt < K && K <= ge) sm.ctl.tk_kth = x;
+                if (gt < K && K <= ge) {
+                    sm.ctl.tk_kth = x;
+                    sm.ctl.tk_cnt = ge;
+                }
             }
             g.sync();
             const float kth = sm.ctl.tk_kth;
-            if (g.t < n && ex.cx[g.t] < kth) ex.cx[g.t] = kNegInf;  // masked: probability 0
-            uint32_t c2 = 0;
+            cnt = (uint32_t)sm.ctl.tk_cnt;
 #pragma unroll
-            for (int e = 0; e < NE; e++) {
+            for (int e = 0; e < NE; e++)
                 if (v[e] < kth) v[e] = kNegInf;
-                c2 += (uint32_t)__builtin_popcountll(__ballot(v[e] != kNegInf));
-            }
-            cnt = g.wsum_u(c2, kSiteCnt2);  // its barrier also orders the masking above
+            g.sync();  // every thread has read the candidates: mask them
+            if (g.t < n && ex.cx[g.t] < kth) ex.cx[g.t] = kNegInf;  // masked: probability 0
             mn = kth;
             cands = true;
             ncand = n;
@@ -927,9 +939,32 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
         for (int j = g.t; j < n; j += kT) ex.cp[j] = ex.cp[j] / sum;  //                 :60
         g.sync();
         if (topp) {  //                                                                 :62-75
-            // stable ascending (p, index) order of the candidates (slot order == index order)
-            for (int j = g.t; j < n; j += kT) ex.cs[seq_rank(ex.cp, n, j)] = (int16_t)j;
+            // Stable ascending (p, index) order of the candidates (slot order == index order).
+            // p = exp(d) / sum never decreases with d = fl32(x - m), so (d, index) order is the
+            // (p, index) order whenever each adjacent pair is in (p, index) order; that is checked,
+            // and the candidates are ranked by p directly otherwise.
+            uint64_t* dkey = reinterpret_cast<uint64_t*>(ex.pre);
+            for (int j = g.t; j < n; j += kT)
+                dkey[j] = ((uint64_t)f2key(ex.cx[j] - m) << 32) | (uint32_t)j;
             g.sync();
+            for (int j = g.t; j < n; j += kT) {
+                const uint64_t kj = dkey[j];
+                int rank = 0;
+#pragma unroll 8
+                for (int l = 0; l < n; l++) rank += dkey[l] < kj ? 1 : 0;
+                ex.cs[rank] = (int16_t)j;
+            }
+            g.sync();
+            bool ok = true;
+            for (int q = g.t; q < n - 1; q += kT) {
+                const int a0 = ex.cs[q], b0 = ex.cs[q + 1];
+                const double pa = ex.cp[a0], pb = ex.cp[b0];
+                ok = ok && (pa < pb || (pa == pb && a0 < b0));
+            }
+            if (g.any(!ok, kSiteTk0 + 2)) {
+                for (int j = g.t; j < n; j += kT) ex.cs[seq_rank(ex.cp, n, j)] = (int16_t)j;
+                g.sync();
+            }
             const double thr = (double)(1.0f - P.top_p);
             // The largest (p, index) entry is the reference's last sorted position, which its
             // loop (j < n - 1) never visits; masked entries sort first with p = 0 and change
