@@ -212,3 +212,37 @@ def test_torch_interop_subprocess():
     p = subprocess.run([sys.executable, script], capture_output=True, text=True, timeout=300)
     print(p.stdout[-2000:], p.stderr[-2000:])
     assert p.returncode == 0
+
+
+def _near_tie_rows(rows, vocab, rng):
+    """Rows whose top-k candidates include values within 1e-38 of the maximum and values far below
+    it (exp underflows): their probabilities tie while d = x - max differs, so the (d, index) order
+    of the candidates is not the reference's (p, index) order and the kernels must rank by p."""
+    x = (rng.standard_normal((rows, vocab)) * 0.5 - 3.0).astype(np.float32)
+    for r in range(rows):
+        cols = rng.choice(vocab, size=12, replace=False)
+        x[r, cols[:6]] = np.array([1e-38, 0.0, 5e-39, -1e-38, 2e-38, 0.0], np.float32)
+        x[r, cols[6:]] = np.array([-900.0, -800.0, -1000.0, -760.0, -3.0e4, -850.0], np.float32)
+        if r % 2:  # a sparse row: 50 ordinary values, the six above and 44 that underflow exp
+            keep = rng.choice(vocab, size=100, replace=False)
+            y = np.full(vocab, -np.inf, np.float32)
+            y[keep[:50]] = rng.standard_normal(50).astype(np.float32)
+            y[keep[50:56]] = x[r, cols[:6]]
+            y[keep[56:]] = (-800.0 - 10.0 * rng.random(44)).astype(np.float32)
+            x[r] = y
+    return x
+
+
+def test_topp_ranks_by_probability_on_near_ties(ctx):
+    rng = np.random.default_rng(321)
+    rows, vocab = 16, 3072
+    x = _near_tie_rows(rows, vocab, rng)
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = 1
+    p["top_k"] = [40, 100, 60, 100, 100, 100, 256, 100] * 2
+    p["top_p"] = [0.9, 0.5, 0.999, 0.3, 0.3, 0.9, 0.3, 0.999] * 2
+    p["temperature"] = 1.0
+    p["rep_penalty"] = 1.0
+    p["keep_id"] = -1
+    p["ban_id"] = -1
+    check(*both(ctx, x, p, np.linspace(0.02, 0.98, rows)), label="near ties")

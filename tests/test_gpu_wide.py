@@ -104,3 +104,31 @@ def test_wide_penalty_only(ctx):
     z = x.copy()
     assert ref.apply_penalty(z, off, hist, 1.05) == 0
     assert np.array_equal(y.view(U32), z.view(U32))
+
+
+def test_wide_topp_ranks_by_probability_on_near_ties(ctx):
+    """Candidates whose probabilities tie while d = x - max differs (values within 1e-38 of the
+    maximum, or far enough below it for exp to underflow): the ordered kernel must rank by p."""
+    rng = np.random.default_rng(654)
+    rows, vocab = 8, 20000
+    x = (rng.standard_normal((rows, vocab)) * 0.5 - 3.0).astype(np.float32)
+    for r in range(rows):
+        cols = rng.choice(vocab, size=12, replace=False)
+        x[r, cols[:6]] = np.array([1e-38, 0.0, 5e-39, -1e-38, 2e-38, 0.0], np.float32)
+        x[r, cols[6:]] = np.array([-900.0, -800.0, -1000.0, -760.0, -3.0e4, -850.0], np.float32)
+        if r % 2:  # a sparse row: 50 ordinary values, the six above and 44 that underflow exp
+            keep = rng.choice(vocab, size=100, replace=False)
+            y = np.full(vocab, -np.inf, np.float32)
+            y[keep[:50]] = rng.standard_normal(50).astype(np.float32)
+            y[keep[50:56]] = x[r, cols[:6]]
+            y[keep[56:]] = (-800.0 - 10.0 * rng.random(44)).astype(np.float32)
+            x[r] = y
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = 1
+    p["top_k"] = [40, 100, 60, 100, 100, 100, 256, 100]
+    p["top_p"] = [0.9, 0.5, 0.999, 0.3, 0.3, 0.9, 0.3, 0.999]
+    p["temperature"] = 1.0
+    p["rep_penalty"] = 1.0
+    p["keep_id"] = -1
+    p["ban_id"] = -1
+    check_rows(ctx, x, p, np.linspace(0.03, 0.97, rows), label="wide near ties")
