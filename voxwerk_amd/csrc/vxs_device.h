@@ -337,29 +337,44 @@ __device__ __forceinline__ int seq_draw(const double* p, const int32_t* id, int 
 // over the recorded prefixes. Same results as seq_topp_cut and seq_draw.
 
 // seq_topp_cut by one wave, on the probabilities already gathered into sorted order
-// (ps[s] = p[order[s]]); scr holds n - 1 doubles of LDS.
+// (ps[s] = p[order[s]]); scr holds n - 1 doubles of LDS. The next batch of eight is read while
+// the current one is added.
 __device__ __forceinline__ int wave_topp_cut(const double* ps, int n, double thr, double* scr, int lane) {
     const int m = n - 1;  // the positions the reference may remove
-    const int z = lane_zero();
     double cum = 0.0;
     int end = 0;  // prefixes recorded
     bool over = false;
-    for (; end + 8 <= m && !over; end += 8) {
-        double c[8];
+    if (m >= 8) {
+        double nx[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            cum += ps[end + k + z];
-            c[k] = cum;
+        for (int k = 0; k < 8; k++) nx[k] = ps[k];
+        while (true) {
+            double cur[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) cur[k] = nx[k];
+            const int nb = end + 8;
+            if (nb + 8 <= m)
+#pragma unroll
+                for (int k = 0; k < 8; k++) nx[k] = ps[nb + k];
+            double c[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                cum += cur[k];
+                c[k] = cum;
+            }
+            if (lane == 0)
+#pragma unroll
+                for (int k = 0; k < 8; k++) scr[end + k] = c[k];
+            end = nb;
+            // the deciding prefix is recorded: the rest exceed thr (or are NaN)
+            over = __builtin_amdgcn_readfirstlane(!(cum <= thr) ? 1 : 0) != 0;
+            if (over || end + 8 > m) break;
         }
-        if (lane == 0)
-#pragma unroll
-            for (int k = 0; k < 8; k++) scr[end + k] = c[k];
-        over = !(cum <= thr);  // the deciding prefix is recorded: the rest exceed thr (or are NaN)
     }
     for (; end < m && !over; end++) {
-        cum += ps[end + z];
+        cum += ps[end];
         if (lane == 0) scr[end] = cum;
-        over = !(cum <= thr);
+        over = __builtin_amdgcn_readfirstlane(!(cum <= thr) ? 1 : 0) != 0;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -371,29 +386,43 @@ __device__ __forceinline__ int wave_topp_cut(const double* ps, int n, double thr
 
 // seq_draw by one wave; scr holds n doubles of LDS. Skipped entries (p <= 0) hold +0 here (the
 // probabilities are exp(d) / sum >= +0, removed ones +0), so adding them leaves the running sum
-// unchanged and the loop adds every entry.
+// unchanged and the loop adds every entry. The next batch of eight is read while the current one
+// is added.
 __device__ __forceinline__ int wave_draw(const double* p, const int32_t* id, int n, double u, double* scr,
                                          int lane) {
-    const int z = lane_zero();
     double acc = 0.0;
     int end = 0;
     bool stop = false;  // a prefix above u (or NaN) is recorded
-    for (; end + 8 <= n && !stop; end += 8) {
-        double c[8];
+    if (n >= 8) {
+        double nx[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            acc += p[end + k + z];
-            c[k] = acc;
+        for (int k = 0; k < 8; k++) nx[k] = p[k];
+        while (true) {
+            double cur[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) cur[k] = nx[k];
+            const int nb = end + 8;
+            if (nb + 8 <= n)
+#pragma unroll
+                for (int k = 0; k < 8; k++) nx[k] = p[nb + k];
+            double c[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                acc += cur[k];
+                c[k] = acc;
+            }
+            if (lane == 0)
+#pragma unroll
+                for (int k = 0; k < 8; k++) scr[end + k] = c[k];
+            end = nb;
+            stop = __builtin_amdgcn_readfirstlane(!(acc <= u) ? 1 : 0) != 0;
+            if (stop || end + 8 > n) break;
         }
-        if (lane == 0)
-#pragma unroll
-            for (int k = 0; k < 8; k++) scr[end + k] = c[k];
-        stop = !(acc <= u);
     }
     for (; end < n && !stop; end++) {
-        acc += p[end + z];
+        acc += p[end];
         if (lane == 0) scr[end] = acc;
-        stop = !(acc <= u);
+        stop = __builtin_amdgcn_readfirstlane(!(acc <= u) ? 1 : 0) != 0;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
