@@ -350,15 +350,15 @@ __device__ __forceinline__ bool build_bitmap(const BlkW& g, const SampleArgs& a,
     __syncthreads();
     const int h0 = a.hist_off[r], h1 = a.hist_off[r + 1];
     bool bad = false;
-    for (int hb = h0; hb < h1; hb += 4 * kTW) {  // four ids per thread in flight
-        int id[4];
+    for (int hb = h0; hb < h1; hb += 8 * kTW) {  // eight ids per thread in flight
+        int id[8];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < 8; k++) {
             const int h = hb + k * kTW + g.t;
             id[k] = h < h1 ? a.hist_ids[h] : 0;
         }
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < 8; k++) {
             if (hb + k * kTW + g.t >= h1) continue;
             if ((unsigned)id[k] >= (unsigned)V) bad = true;
             else atomicOr(&bm[id[k] >> 5], 1u << (id[k] & 31));
@@ -382,7 +382,8 @@ __global__ __launch_bounds__(kTW) void sample_wide_kernel(SampleArgs a, int vec)
     const int r = blockIdx.x;
     const int V = a.vocab;
     const vxs_params P = a.params[(int64_t)r * a.params_stride];
-    if (row_ordered(a, P) && a.out_ids[r] != kPendingId) return;  // served by the ordered kernel
+    const int prior = a.out_ids[r];  // read alongside the options
+    if (row_ordered(a, P) && prior != kPendingId) return;  // served by the ordered kernel
     const float* __restrict__ xrow = a.logits + (int64_t)r * a.ld;
     float* orow = a.out_logits ? a.out_logits + (int64_t)r * V : nullptr;
     double* prow = a.out_probs ? a.out_probs + (int64_t)r * V : nullptr;
@@ -990,6 +991,21 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
         if (g.lane == 0) s.wslot[g.wv] = ((hw >> 4) & 3u) == ((hw >> 16) & 3u) ? 1 : 0;
     }
 
+    // the wave ranges and the row loads (the first sweeps are in flight while the bitmap is built)
+    const int Q = ((V + kTW * 4 - 1) / (kTW * 4)) * 256;  // a wave's range, a multiple of 256
+    const int lo = g.wv * Q, hi = min(V, lo + Q);
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    // raw buffer loads bounded by the row: lanes past its end read zeros instead of faulting
+    const __amdgpu_buffer_rsrc_t rowbuf =
+        __builtin_amdgcn_make_buffer_rsrc((void*)xrow, (short)0, V * (int)sizeof(float), 0x00020000);
+    auto load4 = [&](int base) -> f4 {
+        return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rowbuf, (base + 4 * g.lane) * 4, 0, 2));
+    };
+    constexpr int kPF = 6;  // sweeps in flight per lane
+    f4 cur[kPF];
+#pragma unroll
+    for (int q = 0; q < kPF; q++) cur[q] = load4(lo + q * 256);
+
     RowX X;
     X.bm = nullptr;
     X.rho = P.rep_penalty;
@@ -1009,23 +1025,17 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
     __syncthreads();
 
     // ---- pass A
-    const int Q = ((V + kTW * 4 - 1) / (kTW * 4)) * 256;  // a wave's range, a multiple of 256
-    const int lo = g.wv * Q, hi = min(V, lo + Q);
-    typedef float f4 __attribute__((ext_vector_type(4)));
-    // raw buffer loads bounded by the row: lanes past its end read zeros instead of faulting
-    const __amdgpu_buffer_rsrc_t rowbuf =
-        __builtin_amdgcn_make_buffer_rsrc((void*)xrow, (short)0, V * (int)sizeof(float), 0x00020000);
-    auto load4 = [&](int base) -> f4 {
-        return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rowbuf, (base + 4 * g.lane) * 4, 0, 2));
-    };
     uint32_t* wkey = s.wkey[g.wv];
     int32_t* widx = s.widx[g.wv];
-    bool collect = true;            // false once the wave stops collecting (the general kernel then serves the row)
+    // kStop: the wave stopped collecting (the general kernel then serves the row); kCompacted: its
+    // buffer was compacted at least once. One word, only ever or-ed: two flag variables had their
+    // stores merged behind a selected address, which kept them in scratch memory.
+    constexpr uint32_t kStop = 1u, kCompacted = 2u;
+    uint32_t state = 0;
     int wn = 0;                     // wave-uniform buffer fill
     float tau = -3.402823466e38f;   // entries with fl(x * 1/T) < tau are not candidates ...
     float xt = x_threshold(tau, invT);  // ... which is x < xt
     float M = kNegInf;              // NaN-propagating maximum of the raw entries
-    bool compacted = false;
     // The exact value of entry i: the full transform (penalty, suppression, temperature); entries
     // past the wave's range (the zeros loaded beyond the row end) are -inf.
     auto vexact = [&](int i, float x) -> float { return i < hi ? X(i, x) : kNegInf; };
@@ -1053,7 +1063,7 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
             nf += __builtin_popcountll(__ballot(fin));
         }
         if (nf < K) {
-            collect = false;
+            state |= kStop;
             return;
         }
         // a lower bound of the row's k-th largest that keeps at most k + 32 entries (untied)
@@ -1078,15 +1088,11 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
         tau = key2f(kth);
         xt = x_threshold(tau, invT);
         if (g.lane == 0) atomicMax(&s.tau_key, kth);
-        compacted = true;
+        state |= kCompacted;
     };
     // kPF sweeps in flight per lane: the next group's loads are issued before this group is used
     // (loads past the row return zeros, so they are issued unconditionally)
-    constexpr int kPF = 6;
     {
-        f4 cur[kPF];
-#pragma unroll
-        for (int q = 0; q < kPF; q++) cur[q] = load4(lo + q * 256);
         for (int gb = lo; gb < hi; gb += kPF * 256) {
             // another wave may have raised the shared bound: use it too
             const uint32_t ts = __hip_atomic_load(&s.tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -1100,7 +1106,7 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
 #pragma unroll
             for (int q = 0; q < kPF; q++) {
                 const int base = gb + q * 256;
-                if (base >= hi || !collect) continue;  // (no early exits: they cost structurizer state)
+                if (base >= hi || (state & kStop)) continue;  // (no early exits: they cost structurizer state)
                 const float xv[4] = {cur[q].x, cur[q].y, cur[q].z, cur[q].w};
                 M = __builtin_elementwise_maximum(M, __builtin_elementwise_maximum(xv[0], xv[1]));
                 M = __builtin_elementwise_maximum(M, __builtin_elementwise_maximum(xv[2], xv[3]));
@@ -1112,9 +1118,9 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
                     cnt = 0;
 #pragma unroll
                     for (int j = 0; j < 4; j++) cnt += __builtin_popcountll(__ballot(xv[j] >= xt));
-                    if (wn + cnt > kCapW) collect = false;  // ties: the general kernel
+                    if (wn + cnt > kCapW) state |= kStop;  // ties: the general kernel
                 }
-                if (cnt == 0 || !collect) continue;
+                if (cnt == 0 || (state & kStop)) continue;
                 const int i0 = base + 4 * g.lane;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
@@ -1131,16 +1137,16 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
                 }
                 wn = __builtin_amdgcn_readfirstlane(wn);
             }
-            collect = __builtin_amdgcn_readfirstlane((int)collect) != 0;
-            if (!collect) break;
+            state = __builtin_amdgcn_readfirstlane(state);
+            if (state & kStop) break;
 #pragma unroll
             for (int q = 0; q < kPF; q++) cur[q] = nxt[q];
         }
     }
     // the buffered entries as keys of their exact values, keeping the finite ones at or above the
     // shared bound (a fuller buffer is compacted first, so that the four fit the union's capacity)
-    if (collect && wn > kUnion / kWW) compact();
-    if (collect) {
+    if (!(state & kStop) && wn > kUnion / kWW) compact();
+    if (!(state & kStop)) {
         wave_sync();
         const uint32_t ts = __hip_atomic_load(&s.tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         uint32_t kk[kPerL];
@@ -1172,8 +1178,8 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
         wn = (int)m;
     }
     if (g.lane == 0) {
-        s.wcnt[g.wv] = collect ? wn : -1;
-        s.wcomp[g.wv] = compacted ? 1 : 0;
+        s.wcnt[g.wv] = (state & kStop) ? -1 : wn;
+        s.wcomp[g.wv] = (state & kCompacted) ? 1 : 0;
     }
     // NaN or fl(M * 1/T) = +inf: check the row exactly with the full transform (suppression, or a
     // penalty, may have removed or lowered that value)
