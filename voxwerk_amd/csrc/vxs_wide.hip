@@ -953,13 +953,15 @@ __device__ __forceinline__ float x_threshold(float tau, float invT) {
 // The ordered kernel: the rows row_ordered() selects, in one read of the row.
 //
 // Pass A: each wave streams its quarter of the row and keeps a buffer of raw values and indices.
-// The exact transformed value v = fl(pen(x) * 1/T) is at most fl(x * 1/T), which is monotone in x,
-// so an entry joins the buffer when fl(x * 1/T) >= tau; whenever the buffer cannot take a sweep's
-// entries, the exact values of the buffered entries are formed and the buffer is cut to those >=
-// its k-th largest, which becomes tau (a lower bound of the row's k-th largest, shared between the
-// waves). Sweeps that suppression or the range end touch apply the full transform per entry. NaN
-// reaches the NaN-propagating maximum M of the raw values; fl(M * 1/T) = +inf sends the row
-// through an exact check with the full transform (the penalty may have lowered that value).
+// The exact transformed value v (penalty, suppression, temperature) is at most fl(x * 1/T), which
+// is monotone in the raw x, so an entry joins the buffer when x >= xt, the smallest float with
+// fl(xt * 1/T) >= tau: one compare per entry. Whenever the buffer cannot take a sweep's entries,
+// the exact values of the buffered entries are formed (suppressed entries and those past the
+// wave's range become -inf) and the buffer is cut to a lower bound of its k-th largest (k to
+// k + 32 entries stay), which becomes tau: a lower bound of the row's k-th largest, shared between
+// the waves. NaN and +inf reach the NaN-propagating maximum M of the raw values; M NaN or
+// fl(M * 1/T) = +inf sends the row through an exact check with the full transform (suppression
+// or the penalty may have removed or lowered that value).
 // Tail: one wave finds the k-th largest of the four buffers by a radix select and extracts the
 // candidates; all waves rank them by index and by (d, index), d = v - max; that wave runs the
 // reference's sequential fp64 arithmetic (S6-S8, Sampler.cs:51-87). The (d, index) order is the
@@ -1039,9 +1041,10 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
     // The exact value of entry i: the full transform (penalty, suppression, temperature); entries
     // past the wave's range (the zeros loaded beyond the row end) are -inf.
     auto vexact = [&](int i, float x) -> float { return i < hi ? X(i, x) : kNegInf; };
-    // Keep the buffered entries whose exact value is >= the k-th largest exact value buffered (or
-    // the shared bound, if larger); tau rises to it. With fewer than k finite values buffered the
-    // wave stops collecting.
+    // Keep the buffered entries whose exact value is >= a lower bound of the k-th largest exact
+    // value buffered (one that leaves k to k + 32 of them, ties aside), or the shared bound if that
+    // is larger; tau rises to it. With fewer than k finite values buffered the wave stops
+    // collecting.
     auto compact = [&]() {
         wave_sync();
         uint32_t kk[kPerL];
