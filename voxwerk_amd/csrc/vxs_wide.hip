@@ -1,6 +1,10 @@
 // vxs_wide.hip — the sampler for vocabularies above 8192 (up to 2^19), one 256-thread workgroup
 // per row, streaming the row from HBM instead of holding it in registers.
 //
+// Two kernels run in turn. The ordered kernel (below, sample_wide_ordered_kernel) serves the common
+// sampled top-k rows in one read of the row; the general kernel (sample_wide_kernel) serves every
+// other row and the rows the first one leaves, as follows.
+//
 // Pass A reads the row once (16-byte loads, 1024 entries per sweep) and applies, per entry:
 //   S1 penalty      an LDS bitmap of the history ids marks the entries to rescale (s*rho, or the
 //                   correctly rounded s/rho); each distinct id once by construction  Sampler.cs:25-33
