@@ -31,6 +31,7 @@ sys.path.insert(0, REPO)
 HBM_PEAK_GBPS = 8000.0
 METRIC = "sampled rows/s + HBM GB/s (% peak) at 4096×3072; p50 µs/step at 1 row"
 LLC_BYTES = 256 << 20
+FRAME_ROWS = 24  # sequences of the batched-generation frame step (voice pipeline batch size)
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_full_vocab_nucleus_4096x3072.txt")
 
 
@@ -77,6 +78,22 @@ def native_latency(b, iters):
         return json.loads(p.stdout.strip().splitlines()[-1])
     finally:
         os.unlink(path)
+
+
+def native_frame(rows, iters, serial=False):
+    """One frame step of batched generation over `rows` sequences, timed by the native caller: batched
+    (one call per stage) or serial (one single-row call per sequence and stage); None on failure."""
+    import subprocess
+
+    exe = os.path.join(REPO, "voxwerk_amd", "lib", "vxs_latency")
+    if not os.path.exists(exe):
+        return None
+    p = subprocess.run([exe, "--frame", str(rows), str(iters)] + (["serial"] if serial else []), capture_output=True,
+                       text=True, timeout=300)
+    if p.returncode != 0:
+        log(f"[bench] native frame probe failed: {p.stderr.strip()[:200]}")
+        return None
+    return json.loads(p.stdout.strip().splitlines()[-1])
 
 
 def read_traffic():
@@ -363,6 +380,43 @@ def main() -> int:
                                      "us_per_frame_p50": round(float(frames[len(frames) // 2]), 2),
                                      "us_per_step_p50": round(float(frames[len(frames) // 2]) / w2.steps, 2)}
         log(f"[bench] code predictor frame: p50 {extra[workloads.NAMES[2]]['us_per_frame_p50']:.1f} us")
+        # batched generation: one frame step of 24 sequences (talker stage with resident histories + 15
+        # code-predictor stages), host to host from native code, against the per-row call pattern
+        fb = native_frame(FRAME_ROWS, 500)
+        fs = native_frame(FRAME_ROWS, 100, serial=True)
+        if fb:
+            m = {"workload": f"generate_batch frame step, {FRAME_ROWS} sequences: talker {FRAME_ROWS}x3072 "
+                             f"(resident histories, on-device append) + 15 x {FRAME_ROWS}x2048, host to host, "
+                             f"native caller",
+                 "batched_us_p50": fb["p50_us"], "batched_us_p99": fb["p99_us"],
+                 "batched_calls": fb["calls_per_frame"],
+                 "serial_us_p50": fs["p50_us"] if fs else None, "serial_calls": fs["calls_per_frame"] if fs else None}
+            if not args.no_cpu:
+                from oracle import ref
+
+                rng = np.random.default_rng(0)
+                tx = (rng.random((FRAME_ROWS, 3072), dtype=np.float32) * 6 - 3)
+                cx = (rng.random((15, FRAME_ROWS, 2048), dtype=np.float32) * 6 - 3)
+                tp = np.zeros((), dtype=ref.PARAMS_DTYPE)
+                tp["do_sample"], tp["top_k"], tp["top_p"], tp["temperature"] = 1, 50, 1.0, np.float32(0.9)
+                tp["rep_penalty"], tp["supp_begin"], tp["supp_end"] = np.float32(1.05), 2048, 3072
+                tp["keep_id"], tp["ban_id"] = 2150, -1
+                cp = tp.copy()
+                cp["rep_penalty"], cp["supp_begin"], cp["supp_end"], cp["keep_id"] = np.float32(1.0), 0, 0, -1
+                hoff = np.arange(FRAME_ROWS + 1, dtype=np.int32) * 64
+                hids = rng.integers(0, 2048, FRAME_ROWS * 64).astype(np.int32)
+                reps = []
+                for _ in range(5):
+                    t = time.perf_counter()
+                    ref.sample(tx, tp, rng.random(FRAME_ROWS), hoff, hids, threads=1, want_info=False)
+                    for g in range(15):
+                        ref.sample(cx[g], cp, rng.random(FRAME_ROWS), threads=1, want_info=False)
+                    reps.append(time.perf_counter() - t)
+                m["cpu_oracle_us"] = round(sorted(reps)[2] * 1e6, 1)
+                m["cpu_oracle_sample"] = "the same frame step on the C oracle, 1 thread, 64-id histories, median of 5"
+            extra["generate_batch_frame"] = m
+            log(f"[bench] generate_batch frame ({FRAME_ROWS} sequences): batched p50 {fb['p50_us']:.1f} us "
+                f"({fb['calls_per_frame']} calls), serial p50 {m['serial_us_p50']} us")
 
     traffic = read_traffic()
     out = {

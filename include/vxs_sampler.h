@@ -38,6 +38,7 @@ extern "C" {
 #define VXS_ERR_HIP (-4)             /* HIP runtime failure; text in vxs_last_error                      */
 #define VXS_ERR_UNSUPPORTED (-5)     /* shape outside what this build implements; text in vxs_last_error */
 #define VXS_ERR_NO_DEVICE (-6)       /* no usable gfx950 device                                          */
+#define VXS_ERR_HISTORY_FULL (-7)    /* resident history slot already holds `cap` ids (vxs_sample_batch)  */
 
 /* flags for vxs_sample / vxs_sample_device */
 #define VXS_FLAG_NONE 0u
@@ -138,6 +139,50 @@ VXS_API int vxs_apply_repetition_penalty(vxs_ctx* ctx, int rows, int vocab, floa
 /* First index of the maximum of each host row (Sampler.ArgMax, Sampler.cs:90-95). Synchronous. */
 VXS_API int vxs_argmax(vxs_ctx* ctx, int rows, int vocab, const float* logits, int64_t ld,
                        int32_t* out_ids);
+
+/*
+ * Resident histories for batched generation (TalkerGenerator.GenerateBatch,
+ * TalkerGenerator.cs:322-455). A store holds `slots` sequence histories of at most `cap` ids each
+ * in device memory of the context's device; one slot replaces one Active.History list
+ * (TalkerGenerator.cs:304). The sampler reads a row's history from its slot and appends the id it
+ * draws there (History.Add, TalkerGenerator.cs:374), so histories never cross PCIe per step.
+ * A sequence appends one id per step and retires after MaxNewTokens steps (:375), so
+ * cap = MaxNewTokens always suffices. slots * cap must not exceed 2^31 - 1. All slots start empty.
+ */
+typedef struct vxs_history vxs_history;
+VXS_API int vxs_history_create(vxs_ctx* ctx, int slots, int cap, vxs_history** out);
+/* Frees the store; no work that uses it may still be queued. */
+VXS_API void vxs_history_destroy(vxs_history* h);
+/* Replace slot `slot`'s history with ids[0..n) (0 <= n <= cap; n = 0 empties it, as a refilled
+ * job starts with an empty History, TalkerGenerator.cs:336-349). Stream-ordered; synchronous. */
+VXS_API int vxs_history_set(vxs_ctx* ctx, vxs_history* h, int slot, const int32_t* ids, int n);
+/* Copy slot `slot`'s history into ids[0..max_ids) and its length into *n. Synchronous. */
+VXS_API int vxs_history_get(vxs_ctx* ctx, vxs_history* h, int slot, int32_t* ids, int max_ids, int* n);
+
+/*
+ * One batched sampling stage over host rows whose histories live in `h`: row r penalises with
+ * slot slots[r]'s history, then (append != 0) its sampled id is appended to that slot.
+ * Replaces the serial per-row loops of GenerateBatch: the talker stage (TalkerGenerator.cs:366-375:
+ * ApplyRepetitionPenalty, suppression, a.Sampler.Select, History.Add; append = 1) and the
+ * code-predictor stage (:419-420: SubSampler.Select, no penalty; pass rep_penalty 1 and append = 0).
+ * Arguments as vxs_sample, with `slots` [rows] host memory: distinct slot indices in [0, slots of h).
+ * A row that fails keeps its error code in out_ids and appends nothing; a full slot fails the row
+ * with VXS_ERR_HISTORY_FULL. Synchronous.
+ */
+VXS_API int vxs_sample_batch(vxs_ctx* ctx, vxs_history* h, int rows, int vocab, const float* logits,
+                             int64_t ld, const int32_t* slots, int append, const vxs_params* params,
+                             int params_stride, const double* u, int32_t* out_ids, uint32_t flags);
+
+/*
+ * vxs_sample_batch with device pointers (logits, slots, params, u, out_ids); asynchronous on the
+ * context stream like vxs_sample_device. A slot outside the store fails its row with
+ * VXS_ERR_INVALID_ARG. Slots must be distinct within one call: the store stays in bounds if they
+ * are not, but keeps only one of the ids appended to a repeated slot.
+ */
+VXS_API int vxs_sample_batch_device(vxs_ctx* ctx, vxs_history* h, int rows, int vocab,
+                                    const float* d_logits, int64_t ld, const int32_t* d_slots,
+                                    int append, const vxs_params* d_params, int params_stride,
+                                    const double* d_u, int32_t* d_out_ids, uint32_t flags);
 
 #ifdef __cplusplus
 }

@@ -6,5 +6,5 @@ deterministic synthetic workloads (``workloads``) and the build recipe (``build`
 """
 from . import _lib  # noqa: F401
 
-__all__ = ["sampler", "workloads", "build"]
+__all__ = ["sampler", "generate", "workloads", "build"]
 __version__ = "0.1.0"

@@ -26,6 +26,7 @@ VXS_ERR_NONFINITE = -3
 VXS_ERR_HIP = -4
 VXS_ERR_UNSUPPORTED = -5
 VXS_ERR_NO_DEVICE = -6
+VXS_ERR_HISTORY_FULL = -7
 VXS_FLAG_PATH_BLOCK = 1 << 8
 VXS_FLAG_PATH_WAVE = 1 << 9
 
@@ -90,6 +91,14 @@ _SIGNATURES = {
     "vxs_synchronize": (c_int, [c_void_p]),
     "vxs_apply_repetition_penalty": (c_int, [c_void_p, c_int, c_int, _P, c_int64, _P, _P, c_float]),
     "vxs_argmax": (c_int, [c_void_p, c_int, c_int, _P, c_int64, _P]),
+    "vxs_history_create": (c_int, [c_void_p, c_int, c_int, POINTER(c_void_p)]),
+    "vxs_history_destroy": (None, [c_void_p]),
+    "vxs_history_set": (c_int, [c_void_p, c_void_p, c_int, _P, c_int]),
+    "vxs_history_get": (c_int, [c_void_p, c_void_p, c_int, _P, c_int, POINTER(c_int)]),
+    "vxs_sample_batch": (c_int, [c_void_p, c_void_p, c_int, c_int, _P, c_int64, _P, c_int, _P, c_int, _P, _P,
+                                 c_uint32]),
+    "vxs_sample_batch_device": (c_int, [c_void_p, c_void_p, c_int, c_int, _P, c_int64, _P, c_int, _P, c_int, _P,
+                                        _P, c_uint32]),
 }
 
 

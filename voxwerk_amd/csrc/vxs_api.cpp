@@ -8,6 +8,7 @@
 #include <cstring>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "vxs_internal.h"
 
@@ -16,6 +17,10 @@ namespace {
 constexpr size_t kAlign = 256;
 constexpr int kPolledMaxRows = 1024;                        // host calls below this complete by polling
 constexpr std::chrono::seconds kPollLimit{2};              // then a stream synchronisation takes over
+// Polled calls staging at most this many bytes skip the host-to-device copy: the kernel reads its
+// inputs straight from the coherent pinned staging block over PCIe (one pass, so nothing is lost),
+// which saves the copy's latency (a DMA engine handoff of ~10 us once a copy exceeds a few KiB).
+constexpr size_t kZeroCopyMaxBytes = size_t(2) << 20;
 size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
 
 // Device buffer that only grows.
@@ -80,13 +85,23 @@ struct vxs_ctx {
     DevBuf d_defer;  // deferral list of the one-wave path: 2 counters, then one entry per row
     size_t defer_rows = 0;
     int defer_phase = 0;  // which counter the next call uses
-    HostBuf h_in, h_ids, h_out;
+    HostBuf h_in, h_ids, h_out;  // h_in is coherent: polled calls' kernels read it in place
+    void* h_in_dev = nullptr;    // device address of h_in.p
+    void* h_in_dev_of = nullptr;  // the h_in.p that h_in_dev belongs to
     // completion by polling (small host calls on the one-workgroup-per-row path): a device counter,
     // zeroed once, and coherent pinned memory holding the flag (word 0) and the ids (from word 16)
     DevBuf d_done;
     bool done_ready = false;
     HostBuf h_done;
     int32_t done_seq = 0;
+};
+
+struct vxs_history {
+    int device = 0;
+    int slots = 0;
+    int cap = 0;
+    int32_t* ids = nullptr;  // [slots][cap]
+    int32_t* len = nullptr;  // [slots]
 };
 
 namespace {
@@ -115,6 +130,7 @@ const char* code_text(int code) {
         case VXS_ERR_HIP: return "HIP error";
         case VXS_ERR_UNSUPPORTED: return "unsupported shape";
         case VXS_ERR_NO_DEVICE: return "no gfx950 device";
+        case VXS_ERR_HISTORY_FULL: return "resident history slot is full";
         default: return "error";
     }
 }
@@ -230,14 +246,47 @@ int check_flags(vxs_ctx* ctx, uint32_t flags) {
     return VXS_OK;
 }
 
-// Stage inputs and launch. On success the kernel is queued on ctx->stream.
+// A call whose histories live in a resident store: host slot indices (staged with the inputs),
+// whether to append, and the completion words of a polled call (published by the append kernel).
+struct ResidentCall {
+    const vxs_history* store = nullptr;
+    const int32_t* slots = nullptr;
+    int append = 0;
+    const vxs::SampleArgs* done = nullptr;
+};
+
+// Row histories of a resident call, and the append kernel that follows its sampler.
+void set_resident(vxs::SampleArgs& a, const vxs_history* h, const int32_t* d_slots) {
+    a.hist_off = nullptr;
+    a.hist_ids = h->ids;
+    a.hist_slot = d_slots;
+    a.hist_len = h->len;
+    a.hist_cap = h->cap;
+    a.hist_slots = h->slots;
+}
+
+vxs::AppendArgs append_args(const vxs::SampleArgs& a, const vxs_history* h, int append) {
+    vxs::AppendArgs b{};
+    b.rows = a.rows;
+    b.slots = h->slots;
+    b.cap = h->cap;
+    b.append = append;
+    b.slot = a.hist_slot;
+    b.len = h->len;
+    b.ids = h->ids;
+    b.out_ids = a.out_ids;
+    return b;
+}
+
+// Stage inputs and launch. On success the kernels are queued on ctx->stream.
 int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int64_t ld, const int32_t* hist_off,
                      const int32_t* hist_ids, const vxs_params* params, int params_stride, const double* u,
                      bool want_logits, bool want_probs, uint32_t kflags, uint32_t flags = 0,
-                     const vxs::SampleArgs* done = nullptr) {
+                     const vxs::SampleArgs* done = nullptr, const ResidentCall* res = nullptr) {
     const Layout L = plan(rows, vocab, params_stride, hist_off);
+    const bool zero_copy = (done || (res && res->done)) && L.total <= kZeroCopyMaxBytes;
     VXS_HIP(ctx, ctx->h_in.reserve(L.total));
-    VXS_HIP(ctx, ctx->d_in.reserve(L.total));
+    if (!zero_copy) VXS_HIP(ctx, ctx->d_in.reserve(L.total));
     char* h = static_cast<char*>(ctx->h_in.p);
     for (int i = 0; i < L.np; i++)
         std::memcpy(h + L.params + sizeof(vxs_params) * i, params + (int64_t)i * params_stride, sizeof(vxs_params));
@@ -247,6 +296,8 @@ int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int
     if (hist_off) {
         for (int r = 0; r <= rows; r++) hoff[r] = hist_off[r] - hist_off[0];
         if (L.nh) std::memcpy(h + L.hids, hist_ids + hist_off[0], sizeof(int32_t) * L.nh);
+    } else if (res) {
+        std::memcpy(hoff, res->slots, sizeof(int32_t) * rows);  // slot indices use the offsets' room
     }
     float* lg = reinterpret_cast<float*>(h + L.logits);
     if (ld == L.ld_dev) {
@@ -257,9 +308,17 @@ int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int
     VXS_HIP(ctx, ctx->d_ids.reserve(sizeof(int32_t) * (size_t)rows));
     if (want_logits) VXS_HIP(ctx, ctx->d_logits_out.reserve(sizeof(float) * (size_t)rows * vocab));
     if (want_probs) VXS_HIP(ctx, ctx->d_probs_out.reserve(sizeof(double) * (size_t)rows * vocab));
-    VXS_HIP(ctx, hipMemcpyAsync(ctx->d_in.p, ctx->h_in.p, L.total, hipMemcpyHostToDevice, ctx->stream));
-
-    char* d = static_cast<char*>(ctx->d_in.p);
+    char* d;
+    if (zero_copy) {
+        if (ctx->h_in_dev_of != ctx->h_in.p) {
+            VXS_HIP(ctx, hipHostGetDevicePointer(&ctx->h_in_dev, ctx->h_in.p, 0));
+            ctx->h_in_dev_of = ctx->h_in.p;
+        }
+        d = static_cast<char*>(ctx->h_in_dev);
+    } else {
+        VXS_HIP(ctx, hipMemcpyAsync(ctx->d_in.p, ctx->h_in.p, L.total, hipMemcpyHostToDevice, ctx->stream));
+        d = static_cast<char*>(ctx->d_in.p);
+    }
     vxs::SampleArgs a{};
     a.rows = rows;
     a.vocab = vocab;
@@ -281,8 +340,18 @@ int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int
         a.done_flag = done->done_flag;
         a.done_seq = done->done_seq;
     }
+    if (res) set_resident(a, res->store, reinterpret_cast<const int32_t*>(d + L.hoff));
     if (a.path == vxs::kPathQuad) VXS_HIP(ctx, ensure_defer(ctx, rows, a));
     VXS_HIP(ctx, launch_checked(ctx, a));
+    if (res) {
+        vxs::AppendArgs b = append_args(a, res->store, res->append);
+        if (res->done) {
+            b.host_ids = res->done->out_ids;
+            b.done_flag = res->done->done_flag;
+            b.done_seq = res->done->done_seq;
+        }
+        VXS_HIP(ctx, vxs::launch_history_append(b, ctx->stream));
+    }
     return VXS_OK;
 }
 
@@ -334,6 +403,25 @@ int wait_done(vxs_ctx* ctx, int32_t seq) {
     return VXS_OK;
 }
 
+int check_store(vxs_ctx* ctx, const vxs_history* h) {
+    if (!h) return fail(ctx, VXS_ERR_INVALID_ARG, "history store is NULL");
+    if (h->device != ctx->device) return fail(ctx, VXS_ERR_INVALID_ARG, "history store belongs to another device");
+    return VXS_OK;
+}
+
+// Host slot indices of a resident call: each in [0, slots), no slot twice.
+int check_slots_host(vxs_ctx* ctx, const vxs_history* h, int rows, const int32_t* slots) {
+    if (!slots) return fail(ctx, VXS_ERR_INVALID_ARG, "slots is NULL");
+    std::vector<int32_t> sorted(slots, slots + rows);
+    for (int r = 0; r < rows; r++)
+        if ((unsigned)slots[r] >= (unsigned)h->slots)
+            return fail(ctx, VXS_ERR_INVALID_ARG, "row " + std::to_string(r) + ": slot outside the store");
+    std::sort(sorted.begin(), sorted.end());
+    if (std::adjacent_find(sorted.begin(), sorted.end()) != sorted.end())
+        return fail(ctx, VXS_ERR_INVALID_ARG, "a slot appears twice in one call");
+    return VXS_OK;
+}
+
 // Copy `bytes` of device results into host memory through pinned staging.
 int fetch(vxs_ctx* ctx, void* dst, const void* src, size_t bytes) {
     if (!bytes) return VXS_OK;
@@ -363,6 +451,7 @@ VXS_API int vxs_create(vxs_ctx** out, int device, int max_rows, int max_vocab, i
     vxs_ctx* ctx = new (std::nothrow) vxs_ctx();
     if (!ctx) return VXS_ERR_INVALID_ARG;
     ctx->device = device;
+    ctx->h_in.flags = hipHostMallocCoherent;
     if (hipSetDevice(device) != hipSuccess ||
         hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess) {
         delete ctx;
@@ -546,6 +635,168 @@ VXS_API int vxs_argmax(vxs_ctx* ctx, int rows, int vocab, const float* logits, i
         if ((rc = fetch(ctx, out_ids, ctx->d_ids.p, sizeof(int32_t) * (size_t)rows)) != VXS_OK) return rc;
         ctx->err.clear();
         return first_row_error(ctx, out_ids, rows);
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
+VXS_API int vxs_history_create(vxs_ctx* ctx, int slots, int cap, vxs_history** out) {
+    try {
+        if (!ctx) return VXS_ERR_INVALID_ARG;
+        if (!out) return fail(ctx, VXS_ERR_INVALID_ARG, "out is NULL");
+        *out = nullptr;
+        if (slots <= 0 || cap <= 0) return fail(ctx, VXS_ERR_INVALID_ARG, "slots and cap must be positive");
+        if ((int64_t)slots * cap > INT32_MAX) return fail(ctx, VXS_ERR_INVALID_ARG, "slots * cap exceeds 2^31 - 1");
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        vxs_history* h = new (std::nothrow) vxs_history();
+        if (!h) return fail(ctx, VXS_ERR_INVALID_ARG, "out of host memory");
+        h->device = ctx->device;
+        h->slots = slots;
+        h->cap = cap;
+        hipError_t e = hipMalloc(&h->ids, sizeof(int32_t) * (size_t)slots * (size_t)cap);
+        if (e == hipSuccess) e = hipMalloc(&h->len, sizeof(int32_t) * (size_t)slots);
+        if (e == hipSuccess) e = hipMemsetAsync(h->len, 0, sizeof(int32_t) * (size_t)slots, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) {
+            vxs_history_destroy(h);
+            return hip_fail(ctx, e, "vxs_history_create");
+        }
+        *out = h;
+        ctx->err.clear();
+        return VXS_OK;
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
+VXS_API void vxs_history_destroy(vxs_history* h) {
+    if (!h) return;
+    (void)hipSetDevice(h->device);
+    if (h->ids) (void)hipFree(h->ids);
+    if (h->len) (void)hipFree(h->len);
+    delete h;
+}
+
+VXS_API int vxs_history_set(vxs_ctx* ctx, vxs_history* h, int slot, const int32_t* ids, int n) {
+    try {
+        if (!ctx) return VXS_ERR_INVALID_ARG;
+        int rc = check_store(ctx, h);
+        if (rc != VXS_OK) return rc;
+        if ((unsigned)slot >= (unsigned)h->slots) return fail(ctx, VXS_ERR_INVALID_ARG, "slot outside the store");
+        if (n < 0 || n > h->cap) return fail(ctx, VXS_ERR_INVALID_ARG, "n outside [0, cap]");
+        if (n > 0 && !ids) return fail(ctx, VXS_ERR_INVALID_ARG, "ids is NULL");
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        VXS_HIP(ctx, ctx->h_ids.reserve(sizeof(int32_t) * ((size_t)n + 1)));
+        int32_t* st = static_cast<int32_t*>(ctx->h_ids.p);
+        st[0] = n;
+        if (n) std::memcpy(st + 1, ids, sizeof(int32_t) * (size_t)n);
+        if (n)
+            VXS_HIP(ctx, hipMemcpyAsync(h->ids + (int64_t)slot * h->cap, st + 1, sizeof(int32_t) * (size_t)n,
+                                        hipMemcpyHostToDevice, ctx->stream));
+        VXS_HIP(ctx, hipMemcpyAsync(h->len + slot, st, sizeof(int32_t), hipMemcpyHostToDevice, ctx->stream));
+        VXS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        ctx->err.clear();
+        return VXS_OK;
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
+VXS_API int vxs_history_get(vxs_ctx* ctx, vxs_history* h, int slot, int32_t* ids, int max_ids, int* n) {
+    try {
+        if (!ctx) return VXS_ERR_INVALID_ARG;
+        int rc = check_store(ctx, h);
+        if (rc != VXS_OK) return rc;
+        if ((unsigned)slot >= (unsigned)h->slots) return fail(ctx, VXS_ERR_INVALID_ARG, "slot outside the store");
+        if (max_ids < 0 || (max_ids > 0 && !ids)) return fail(ctx, VXS_ERR_INVALID_ARG, "bad ids / max_ids");
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        int32_t len = 0;
+        if ((rc = fetch(ctx, &len, h->len + slot, sizeof(int32_t))) != VXS_OK) return rc;
+        len = std::min(std::max(len, 0), h->cap);
+        const int k = std::min(len, max_ids);
+        if (k && (rc = fetch(ctx, ids, h->ids + (int64_t)slot * h->cap, sizeof(int32_t) * (size_t)k)) != VXS_OK)
+            return rc;
+        if (n) *n = len;
+        ctx->err.clear();
+        return VXS_OK;
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
+VXS_API int vxs_sample_batch(vxs_ctx* ctx, vxs_history* h, int rows, int vocab, const float* logits, int64_t ld,
+                             const int32_t* slots, int append, const vxs_params* params, int params_stride,
+                             const double* u, int32_t* out_ids, uint32_t flags) {
+    try {
+        int rc = check_shape(ctx, rows, vocab, logits, ld, params, params_stride, out_ids);
+        if (rc != VXS_OK) return rc;
+        if ((rc = check_flags(ctx, flags)) != VXS_OK) return rc;
+        if ((rc = check_store(ctx, h)) != VXS_OK) return rc;
+        if (rows == 0) return VXS_OK;
+        if ((rc = check_params_host(ctx, rows, params, params_stride, u)) != VXS_OK) return rc;
+        if ((rc = check_slots_host(ctx, h, rows, slots)) != VXS_OK) return rc;
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        ResidentCall res;
+        res.store = h;
+        res.slots = slots;
+        res.append = append != 0;
+        if (polled_call(rows, vocab, flags, false, false)) {
+            vxs::SampleArgs done{};
+            VXS_HIP(ctx, ensure_done(ctx, rows, done));
+            res.done = &done;
+            rc = stage_and_launch(ctx, rows, vocab, logits, ld, nullptr, nullptr, params, params_stride, u, false,
+                                  false, 0, flags, nullptr, &res);
+            if (rc != VXS_OK) {
+                ctx->done_ready = false;
+                return rc;
+            }
+            if ((rc = wait_done(ctx, done.done_seq)) != VXS_OK) return rc;
+            std::memcpy(out_ids, done.out_ids, sizeof(int32_t) * (size_t)rows);
+            ctx->err.clear();
+            return first_row_error(ctx, out_ids, rows);
+        }
+        rc = stage_and_launch(ctx, rows, vocab, logits, ld, nullptr, nullptr, params, params_stride, u, false, false,
+                              0, flags, nullptr, &res);
+        if (rc != VXS_OK) return rc;
+        if ((rc = fetch(ctx, out_ids, ctx->d_ids.p, sizeof(int32_t) * (size_t)rows)) != VXS_OK) return rc;
+        ctx->err.clear();
+        return first_row_error(ctx, out_ids, rows);
+    } catch (const std::exception& e) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, e.what());
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
+VXS_API int vxs_sample_batch_device(vxs_ctx* ctx, vxs_history* h, int rows, int vocab, const float* d_logits,
+                                    int64_t ld, const int32_t* d_slots, int append, const vxs_params* d_params,
+                                    int params_stride, const double* d_u, int32_t* d_out_ids, uint32_t flags) {
+    try {
+        int rc = check_shape(ctx, rows, vocab, d_logits, ld, d_params, params_stride, d_out_ids);
+        if (rc != VXS_OK) return rc;
+        if ((rc = check_flags(ctx, flags)) != VXS_OK) return rc;
+        if ((rc = check_store(ctx, h)) != VXS_OK) return rc;
+        if (rows == 0) return VXS_OK;
+        if (!d_slots) return fail(ctx, VXS_ERR_INVALID_ARG, "slots is NULL");
+        if (params_stride > 1) return fail(ctx, VXS_ERR_INVALID_ARG, "device params_stride must be 0 or 1");
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        vxs::SampleArgs a{};
+        a.rows = rows;
+        a.vocab = vocab;
+        a.ld = ld;
+        a.logits = d_logits;
+        set_resident(a, h, d_slots);
+        a.params = d_params;
+        a.params_stride = params_stride;
+        a.u = d_u;
+        a.out_ids = d_out_ids;
+        a.kflags = 0;
+        a.path = choose_path(flags, rows, vocab);
+        if (a.path == vxs::kPathQuad) VXS_HIP(ctx, ensure_defer(ctx, rows, a));
+        VXS_HIP(ctx, launch_checked(ctx, a));
+        VXS_HIP(ctx, vxs::launch_history_append(append_args(a, h, append != 0), ctx->stream));
+        ctx->err.clear();
+        return VXS_OK;
     } catch (...) {
         return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
     }

@@ -20,6 +20,13 @@ struct SampleArgs {
     const float* logits;
     const int32_t* hist_off;
     const int32_t* hist_ids;
+    // Resident histories (vxs_history), used instead of hist_off when hist_len is set: row r reads
+    // slot s = hist_slot[r], the ids hist_ids[s * hist_cap, s * hist_cap + min(hist_len[s], hist_cap)).
+    // A slot outside [0, hist_slots) reads as empty; the append kernel then fails the row.
+    const int32_t* hist_slot;
+    const int32_t* hist_len;
+    int hist_cap;
+    int hist_slots;
     const vxs_params* params;
     int params_stride;
     const double* u;
@@ -55,8 +62,45 @@ constexpr int kWaveMaxVocab = 3072;
 // Largest vocabulary of the streaming kernel (vxs_wide.hip); its history bitmap lives in LDS.
 constexpr int kWideMaxVocab = 1 << 19;
 
+// Whether row histories are given (CSR offsets or a resident store).
+__device__ __forceinline__ bool has_history(const SampleArgs& a) {
+    return a.hist_off != nullptr || a.hist_len != nullptr;
+}
+
+// The history of row r: ids a.hist_ids[h0, h1). Wave-uniform (scalar loads).
+struct HistRange {
+    int h0, h1;
+};
+__device__ __forceinline__ HistRange history_range(const SampleArgs& a, int r) {
+    if (!a.hist_len) return {a.hist_off[r], a.hist_off[r + 1]};
+    const int s = a.hist_slot[r];
+    const bool ok = (unsigned)s < (unsigned)a.hist_slots;
+    const int h0 = ok ? s * a.hist_cap : 0;
+    const int n = ok ? a.hist_len[s] : 0;
+    return {h0, h0 + min(max(n, 0), a.hist_cap)};
+}
+
+// Resident-history step after a sampling launch: per row, fail a row whose slot lies outside
+// [0, slots); when `append`, add a sampled id (>= 0) to its slot, or fail the row with
+// VXS_ERR_HISTORY_FULL when the slot holds `cap` ids. With `host_ids`, one workgroup handles every
+// row, copies the final ids there and then stores `done_seq` to `done_flag` (a host-polled call).
+struct AppendArgs {
+    int rows;
+    int slots;
+    int cap;
+    int append;
+    const int32_t* slot;
+    int32_t* len;
+    int32_t* ids;
+    int32_t* out_ids;
+    int32_t* host_ids;
+    int32_t* done_flag;
+    int32_t done_seq;
+};
+
 // Enqueue the sampler on `stream`. Returns hipSuccess or the launch error.
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream);
 hipError_t launch_sample_wide(const SampleArgs& a, hipStream_t stream);
+hipError_t launch_history_append(const AppendArgs& a, hipStream_t stream);
 
 }  // namespace vxs

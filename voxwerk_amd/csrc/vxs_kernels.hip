@@ -518,15 +518,16 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
     const int V = a.vocab;
     const vxs_params P = a.params[(int64_t)r * a.params_stride];
     const float* __restrict__ xrow = a.logits + (int64_t)r * a.ld;
-    const bool pen_on = P.rep_penalty != 1.0f && a.hist_off != nullptr;
+    const bool pen_on = P.rep_penalty != 1.0f && has_history(a);
 
     // ---- issue the history prefetch and the row loads together
     constexpr int HP = 2;  // ids per thread fetched up front (512 per row)
     int h0 = 0, h1 = 0;
     int pre[HP];
     if (pen_on) {
-        h0 = a.hist_off[r];
-        h1 = a.hist_off[r + 1];
+        const HistRange hr = history_range(a, r);
+        h0 = hr.h0;
+        h1 = hr.h1;
 #pragma unroll
         for (int k = 0; k < HP; k++) {
             const int h = h0 + g.t + k * kT;

@@ -5,17 +5,124 @@
 // input file (little-endian): int32 rows, int32 vocab, int32 hist_len, then rows*vocab float32 logits,
 // rows*hist_len int32 history ids, rows vxs_params, rows float64 uniforms.
 // output: one JSON line {"p50_us": .., "p99_us": .., "iters": .., "id0": ..}
+//
+// usage: vxs_latency --frame <rows> <iterations> [serial]
+// One frame step of batched generation (TalkerGenerator.GenerateBatch, TalkerGenerator.cs:362-426)
+// over `rows` sequences: the talker stage (rows x 3072, penalty over resident histories, suppression,
+// append) and 15 code-predictor stages (rows x 2048), each one batched call. With "serial", the same
+// work as the reference's per-row loops: one single-row call per sequence and stage, histories
+// passed from the host. Synthetic logits; output {"p50_us": .., "p99_us": .., "iters": .., "calls": ..}.
 #include <algorithm>
 #include <chrono>
+#include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <vector>
 
 #include "vxs_sampler.h"
 
+namespace {
+
+constexpr int kTalkerVocab = 3072, kCpVocab = 2048, kGroups = 16, kEos = 2150;
+
+// xorshift64* in [0, 1)
+struct Rng {
+    uint64_t s;
+    double next() {
+        s ^= s >> 12;
+        s ^= s << 25;
+        s ^= s >> 27;
+        return (double)((s * 0x2545F4914F6CDD1DULL) >> 11) * 0x1.0p-53;
+    }
+};
+
+int frame_mode(int rows, int iters, bool serial) {
+    Rng rng{0x9E3779B97F4A7C15ULL};
+    std::vector<float> talker((size_t)rows * kTalkerVocab), cp((size_t)kGroups * rows * kCpVocab);
+    for (float& x : talker) x = (float)(6.0 * rng.next() - 3.0);
+    for (float& x : cp) x = (float)(6.0 * rng.next() - 3.0);
+    const vxs_params tp{1, 50, 1.0f, 0.9f, 1.05f, kTalkerVocab - 1024, kTalkerVocab, kEos, -1};
+    const vxs_params cpp{1, 50, 1.0f, 0.9f, 1.0f, 0, 0, -1, -1};
+    std::vector<vxs_params> tps(rows, tp), cps(rows, cpp);
+    std::vector<double> u(rows);
+    std::vector<int32_t> ids(rows), slots(rows);
+    for (int r = 0; r < rows; r++) slots[r] = r;
+    const int warm = 50, total = warm + iters;
+
+    vxs_ctx* ctx = nullptr;
+    if (vxs_create(&ctx, 0, rows, kTalkerVocab, 0) != VXS_OK) {
+        std::fprintf(stderr, "vxs_create failed\n");
+        return 1;
+    }
+    vxs_history* store = nullptr;
+    if (vxs_history_create(ctx, rows, total + 1, &store) != VXS_OK) {
+        std::fprintf(stderr, "vxs_history_create failed: %s\n", vxs_last_error(ctx));
+        vxs_destroy(ctx);
+        return 1;
+    }
+    std::vector<std::vector<int32_t>> hist(rows);  // host histories of the serial loop
+    long calls = 0;
+    auto step = [&]() -> int {
+        for (int r = 0; r < rows; r++) u[r] = rng.next();
+        int rc;
+        if (!serial) {
+            rc = vxs_sample_batch(ctx, store, rows, kTalkerVocab, talker.data(), kTalkerVocab, slots.data(), 1,
+                                  tps.data(), 1, u.data(), ids.data(), 0);
+            calls++;
+            for (int g = 1; g < kGroups && rc == VXS_OK; g++, calls++) {
+                for (int r = 0; r < rows; r++) u[r] = rng.next();
+                rc = vxs_sample(ctx, rows, kCpVocab, cp.data() + (size_t)g * rows * kCpVocab, kCpVocab, nullptr,
+                                nullptr, cps.data(), 1, u.data(), ids.data(), nullptr, nullptr, 0);
+            }
+            return rc;
+        }
+        for (int r = 0; r < rows; r++, calls++) {
+            const int32_t off[2] = {0, (int32_t)hist[r].size()};
+            int32_t id = 0;
+            rc = vxs_sample(ctx, 1, kTalkerVocab, talker.data() + (size_t)r * kTalkerVocab, kTalkerVocab, off,
+                            hist[r].data(), &tp, 0, &u[r], &id, nullptr, nullptr, 0);
+            if (rc != VXS_OK) return rc;
+            hist[r].push_back(id);
+        }
+        for (int g = 1; g < kGroups; g++)
+            for (int r = 0; r < rows; r++, calls++) {
+                const double ur = rng.next();
+                int32_t id = 0;
+                rc = vxs_sample(ctx, 1, kCpVocab, cp.data() + ((size_t)g * rows + r) * kCpVocab, kCpVocab, nullptr,
+                                nullptr, &cpp, 0, &ur, &id, nullptr, nullptr, 0);
+                if (rc != VXS_OK) return rc;
+            }
+        return VXS_OK;
+    };
+    std::vector<double> t;
+    int rc = VXS_OK;
+    for (int i = 0; i < total && rc == VXS_OK; i++) {
+        const auto a = std::chrono::steady_clock::now();
+        rc = step();
+        if (i >= warm) t.push_back(std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - a).count());
+    }
+    if (rc != VXS_OK) std::fprintf(stderr, "sampling failed: %s\n", vxs_last_error(ctx));
+    vxs_history_destroy(store);
+    vxs_destroy(ctx);
+    if (rc != VXS_OK) return 1;
+    std::sort(t.begin(), t.end());
+    std::printf("{\"p50_us\": %.2f, \"p99_us\": %.2f, \"iters\": %d, \"calls_per_frame\": %ld}\n", t[t.size() / 2],
+                t[(size_t)(t.size() * 0.99)], iters, calls / total);
+    return 0;
+}
+
+}  // namespace
+
 int main(int argc, char** argv) {
+    if (argc >= 4 && std::strcmp(argv[1], "--frame") == 0) {
+        const int rows = std::atoi(argv[2]), iters = std::atoi(argv[3]);
+        if (rows <= 0 || iters <= 0) return 2;
+        return frame_mode(rows, iters, argc >= 5 && std::strcmp(argv[4], "serial") == 0);
+    }
     if (argc < 3) {
-        std::fprintf(stderr, "usage: %s <input file> <iterations>\n", argv[0]);
+        std::fprintf(stderr, "usage: %s <input file> <iterations> | --frame <rows> <iterations> [serial]\n", argv[0]);
         return 2;
     }
     std::FILE* f = std::fopen(argv[1], "rb");

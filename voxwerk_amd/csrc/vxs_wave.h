@@ -129,12 +129,14 @@ __device__ __forceinline__ int wave_prepare(const SampleArgs& a, int r, int lane
     using namespace wave;
     if (a.out_logits || a.out_probs || (a.kflags & KF_STOP_AFTER_PENALTY)) return 1;
     if (P.do_sample && P.top_k > 0 && P.top_k < a.vocab) return 1;
-    w.pen_on = P.rep_penalty != 1.0f && a.hist_off != nullptr;
-    w.h0 = w.h1 = 0;
-    if (w.pen_on) {
-        w.h0 = a.hist_off[r];
-        w.h1 = a.hist_off[r + 1];
-        if (w.h1 - w.h0 > kHP * 64) return 1;  // long history
+    const bool pen_on = P.rep_penalty != 1.0f && has_history(a);
+    HistRange hr{0, 0};
+    if (pen_on) hr = history_range(a, r);
+    w.pen_on = pen_on;  // each field written once: no selected-address stores
+    w.h0 = hr.h0;
+    w.h1 = hr.h1;
+    if (hr.h1 - hr.h0 > kHP * 64) return 1;  // long history
+    if (pen_on) {
 #pragma unroll
         for (int k = 0; k < kHP; k++) {
             const int h = w.h0 + lane + k * 64;

@@ -341,7 +341,7 @@ __device__ __forceinline__ float row_inv_temp(const vxs_params& P) {
 __device__ __forceinline__ bool row_ordered(const SampleArgs& a, const vxs_params& P) {
     if (a.kflags & KF_STOP_AFTER_PENALTY) return false;
     const float invT = row_inv_temp(P);
-    const bool has_pen = P.rep_penalty != 1.0f && a.hist_off != nullptr;
+    const bool has_pen = P.rep_penalty != 1.0f && has_history(a);
     return P.do_sample && P.top_k > 0 && P.top_k <= kKMax && P.top_k < a.vocab && invT > 0.0f &&
            invT < kPosInf && (!has_pen || P.rep_penalty >= 1.0f);
 }
@@ -352,7 +352,8 @@ __device__ __forceinline__ bool build_bitmap(const BlkW& g, const SampleArgs& a,
     const int words = ((V + 31) >> 5) + kBmPad;
     for (int w = g.t; w < words; w += kTW) bm[w] = 0;
     __syncthreads();
-    const int h0 = a.hist_off[r], h1 = a.hist_off[r + 1];
+    const HistRange hr = history_range(a, r);
+    const int h0 = hr.h0, h1 = hr.h1;
     bool bad = false;
     for (int hb = h0; hb < h1; hb += 8 * kTW) {  // eight ids per thread in flight
         int id[8];
@@ -399,7 +400,7 @@ __global__ __launch_bounds__(kTW) void sample_wide_kernel(SampleArgs a, int vec)
     X.rho = P.rep_penalty;
     X.rinv = 1.0f / P.rep_penalty;
     X.fastdiv = __builtin_fabsf(P.rep_penalty) >= 0x1p-60f && __builtin_fabsf(P.rep_penalty) <= 0x1p60f;
-    if (P.rep_penalty != 1.0f && a.hist_off != nullptr) {
+    if (P.rep_penalty != 1.0f && has_history(a)) {
         if (!build_bitmap(g, a, r, V, bm_dyn)) return;
         X.bm = bm_dyn;
     }
@@ -1017,7 +1018,7 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
     X.rho = P.rep_penalty;
     X.rinv = 1.0f / P.rep_penalty;
     X.fastdiv = __builtin_fabsf(P.rep_penalty) >= 0x1p-60f && __builtin_fabsf(P.rep_penalty) <= 0x1p60f;
-    if (P.rep_penalty != 1.0f && a.hist_off != nullptr) {
+    if (P.rep_penalty != 1.0f && has_history(a)) {
         if (!build_bitmap(g, a, r, V, bm_dyn)) return;
         X.bm = bm_dyn;
     }

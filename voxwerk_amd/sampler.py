@@ -35,7 +35,13 @@ class NonFiniteLogits(SamplerError, ValueError):
     """NaN or +inf after temperature scaling: outside the sampler contract."""
 
 
+class HistoryFull(SamplerError, OverflowError):
+    """A resident history slot already holds its capacity of ids (vxs_sample_batch)."""
+
+
 def _raise(code: int, message: str) -> None:
+    if code == _lib.VXS_ERR_HISTORY_FULL:
+        raise HistoryFull(code, message)
     if code == _lib.VXS_ERR_ID_OUT_OF_RANGE:
         raise HistoryIdOutOfRange(code, message)
     if code == _lib.VXS_ERR_NONFINITE:
@@ -303,6 +309,99 @@ class Context:
         self._check(self._lib.vxs_argmax(self._h, x.shape[0], x.shape[1], ptr(x), x.shape[1], ptr(ids)))
         return ids
 
+    # resident histories ----------------------------------------------------------------------------
+    def history(self, slots: int, cap: int) -> "HistoryStore":
+        """A resident history store on this context's device (vxs_history_create)."""
+        return HistoryStore(self, slots, cap)
+
+    def sample_batch(self, store: "HistoryStore", logits: np.ndarray, slots, params: np.ndarray,
+                     u: Optional[np.ndarray] = None, append: bool = True, raise_on_error: bool = True,
+                     path: str = "auto") -> np.ndarray:
+        """One batched stage over host rows whose histories live in `store`: row r penalises with
+        slot slots[r] and, with `append`, its id is added to that slot (vxs_sample_batch)."""
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        if logits.ndim == 1:
+            logits = logits.reshape(1, -1)
+        rows, vocab = logits.shape
+        slots = np.ascontiguousarray(slots, dtype=np.int32).reshape(-1)
+        if slots.shape[0] != rows:
+            raise ValueError("slots must have one entry per row")
+        params = np.ascontiguousarray(params, dtype=PARAMS_DTYPE)
+        stride = 0 if params.ndim == 0 or params.size == 1 else 1
+        if stride and params.shape[0] != rows:
+            raise ValueError("params must be one record or one per row")
+        if u is not None:
+            u = np.ascontiguousarray(u, dtype=np.float64).reshape(-1)
+            if u.shape[0] != rows:
+                raise ValueError("u must have one value per row")
+        ids = np.empty(rows, dtype=np.int32)
+        rc = self._lib.vxs_sample_batch(self._h, store.handle, rows, vocab, ptr(logits), vocab, ptr(slots),
+                                        1 if append else 0, ptr(params), stride, ptr(u), ptr(ids), PATH_FLAGS[path])
+        if rc != 0 and (raise_on_error or rc not in (_lib.VXS_ERR_ID_OUT_OF_RANGE, _lib.VXS_ERR_NONFINITE,
+                                                     _lib.VXS_ERR_HISTORY_FULL)):
+            _raise(rc, self.last_error())
+        return ids
+
+    def sample_batch_device(self, store: "HistoryStore", rows: int, vocab: int, logits, ld: int, slots, params,
+                            params_stride: int, u, out_ids, append: bool = True, path: str = "auto") -> None:
+        """vxs_sample_batch_device: device pointers (torch tensors or ints), asynchronous."""
+        rc = self._lib.vxs_sample_batch_device(self._h, store.handle, rows, vocab, ptr(logits), ld, ptr(slots),
+                                               1 if append else 0, ptr(params), params_stride, ptr(u),
+                                               ptr(out_ids), PATH_FLAGS[path])
+        self._check(rc)
+
+
+class HistoryStore:
+    """Device-resident histories (vxs_history): ``slots`` sequences of at most ``cap`` ids each, all
+    empty at creation. One slot stands for one ``Active.History`` list of GenerateBatch
+    (TalkerGenerator.cs:304); the sampler appends to it on the device (History.Add, :374)."""
+
+    def __init__(self, context: Context, slots: int, cap: int):
+        self._ctx = context
+        self._lib = context._lib
+        h = ctypes.c_void_p()
+        context._check(self._lib.vxs_history_create(context.handle, slots, cap, ctypes.byref(h)))
+        self._h = h
+        self.slots = slots
+        self.cap = cap
+
+    @property
+    def handle(self):
+        return self._h
+
+    def set(self, slot: int, ids: Iterable[int] = ()) -> None:
+        """Replace one slot's history (an empty one for a newly started sequence)."""
+        a = np.ascontiguousarray(list(ids), dtype=np.int32)
+        self._ctx._check(self._lib.vxs_history_set(self._ctx.handle, self._h, slot, ptr(a) if a.size else None,
+                                                   int(a.size)))
+
+    def get(self, slot: int) -> np.ndarray:
+        n = ctypes.c_int(0)
+        self._ctx._check(self._lib.vxs_history_get(self._ctx.handle, self._h, slot, None, 0, ctypes.byref(n)))
+        out = np.empty(n.value, dtype=np.int32)
+        if n.value:
+            self._ctx._check(self._lib.vxs_history_get(self._ctx.handle, self._h, slot, ptr(out), n.value,
+                                                       ctypes.byref(n)))
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._ctx.synchronize()
+            self._lib.vxs_history_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
 
 _default: dict[int, Context] = {}
 _default_lock = threading.Lock()
@@ -339,6 +438,11 @@ class Sampler:
         ctx = context or default_context()
         hist = np.asarray(list(history), dtype=np.int32)
         ctx.apply_repetition_penalty(logits, np.array([0, hist.size], np.int32), hist, penalty)
+
+    def NextUniform(self, opts: SamplingOptions) -> float:
+        """The uniform one ``Select(logits, opts)`` would consume (none, returned as 0, when greedy);
+        batched callers draw each row's uniform from its own sequence's Sampler with it."""
+        return self._rng.NextDouble() if opts.DoSample else 0.0
 
     def Select(self, logits: np.ndarray, opts: SamplingOptions) -> int:
         """Select one id from a float32 row; the row is updated in place the way the C# span is
