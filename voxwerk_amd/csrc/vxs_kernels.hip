@@ -516,24 +516,10 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
     auto eidx = [&](int e) { return (e >> 2) * kSW + g.t * 4 + (e & 3); };
 
     const int V = a.vocab;
-    const vxs_params P = a.params[(int64_t)r * a.params_stride];
     const float* __restrict__ xrow = a.logits + (int64_t)r * a.ld;
-    const bool pen_on = P.rep_penalty != 1.0f && has_history(a);
 
-    // ---- issue the history prefetch and the row loads together
-    constexpr int HP = 2;  // ids per thread fetched up front (512 per row)
-    int h0 = 0, h1 = 0;
-    int pre[HP];
-    if (pen_on) {
-        const HistRange hr = history_range(a, r);
-        h0 = hr.h0;
-        h1 = hr.h1;
-#pragma unroll
-        for (int k = 0; k < HP; k++) {
-            const int h = h0 + g.t + k * kT;
-            pre[k] = h < h1 ? a.hist_ids[h] : 0;
-        }
-    }
+    // ---- the row loads first, then the options and the history range (independent of each
+    // other, so that inputs read over PCIe cost one round trip before the history ids)
     float v[NE];
 #pragma unroll
     for (int c = 0; c < NC; c++) {
@@ -552,6 +538,20 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
     }
     // entries past the vocabulary (pads of the last sweep) hold -inf: they never win, carry no mass
     // and are never written back
+    const vxs_params P = a.params[(int64_t)r * a.params_stride];
+    HistRange hr{0, 0};
+    if (has_history(a)) hr = history_range(a, r);
+    const bool pen_on = P.rep_penalty != 1.0f && has_history(a);
+    constexpr int HP = 2;  // ids per thread fetched up front (512 per row)
+    const int h0 = hr.h0, h1 = pen_on ? hr.h1 : hr.h0;
+    int pre[HP];
+    if (pen_on) {
+#pragma unroll
+        for (int k = 0; k < HP; k++) {
+            const int h = h0 + g.t + k * kT;
+            pre[k] = h < h1 ? a.hist_ids[h] : 0;
+        }
+    }
 
     // ---- S1: repetition penalty over the distinct history ids
     if (pen_on && h1 > h0) {
@@ -1308,7 +1308,7 @@ __device__ __forceinline__ void signal_done(const SampleArgs& a) {
     __threadfence_system();  // this thread's id store is visible to the host before the count
     __syncthreads();
     if (threadIdx.x == 0) {
-        const int prev = atomicAdd(a.done_count, 1);
+        const int prev = gridDim.x == 1 ? 0 : atomicAdd(a.done_count, 1);  // one workgroup: no count
         if (prev == (int)gridDim.x - 1) {
             *a.done_count = 0;  // the next call (stream-ordered after this one) starts from zero
             __threadfence_system();
