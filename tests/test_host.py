@@ -122,6 +122,27 @@ def test_dotnet_random_first_values():
     assert DotNetRandom(42).Next() == 1434747710
 
 
+def test_dotnet_random_large_seeds_stay_in_range():
+    """Seeds above MSEED overflow 32-bit arithmetic during seeding; C# wraps (unchecked int), and
+    every InternalSample then stays in [0, int.MaxValue). A version with unbounded integers returns
+    negative samples for most such seeds, which this catches."""
+    rng = np.random.default_rng(0)
+    seeds = [2**31 - 1, -(2**31), 10**9, 2 * 10**9, 161803399] + rng.integers(-2**31, 2**31, 200).tolist()
+    for seed in seeds:
+        r = DotNetRandom(int(seed))
+        xs = [r.Next() for _ in range(200)]
+        assert all(0 <= x < DotNetRandom.MBIG for x in xs), seed
+
+
+def test_sub_seed_wraps_like_csharp():
+    from voxwerk_amd.generate import _sub_seed
+    from voxwerk_amd.sampler import GenerationOptions
+
+    assert _sub_seed(GenerationOptions(Seed=7)) == 8
+    assert _sub_seed(GenerationOptions(Seed=2**31 - 1)) == -(2**31)
+    assert _sub_seed(GenerationOptions()) is None
+
+
 def test_dotnet_random_next_double_range_and_determinism():
     a, b = DotNetRandom(7), DotNetRandom(7)
     xs = [a.NextDouble() for _ in range(10000)]

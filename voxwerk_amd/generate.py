@@ -59,7 +59,10 @@ class _Active:
 
 
 def _sub_seed(opts: GenerationOptions) -> Optional[int]:
-    return opts.Seed + 1 if opts.Seed is not None else None  # TalkerGenerator.cs:218, :346
+    """``Seed + 1`` in C#'s unchecked int arithmetic (TalkerGenerator.cs:218, :346)."""
+    if opts.Seed is None:
+        return None
+    return ((opts.Seed + 1 + 0x80000000) & 0xFFFFFFFF) - 0x80000000
 
 
 def generate(job: int, opts: GenerationOptions, model: TalkerModel, context: Optional[Context] = None,

@@ -116,10 +116,16 @@ def sub_talker_params(opts: GenerationOptions) -> np.ndarray:
 # ---------------------------------------------------------------------------------------------
 # .NET System.Random(seed) — legacy subtractive generator, so seeded runs reproduce the C# draws
 # ---------------------------------------------------------------------------------------------
+def _i32(x: int) -> int:
+    """C#'s unchecked ``int`` arithmetic: wrap to [-2^31, 2^31)."""
+    return ((x + 0x80000000) & 0xFFFFFFFF) - 0x80000000
+
+
 class DotNetRandom:
     """``new Random(seed)`` as .NET constructs it for an explicit seed (Knuth's subtractive method,
     MSEED = 161803398). ``NextDouble()`` = InternalSample() / int.MaxValue. Sampler.cs:21,77 consume one
-    NextDouble per sampled Select."""
+    NextDouble per sampled Select. Every step wraps to 32 bits as C#'s unchecked ``int`` arithmetic
+    does: for seeds above MSEED the seeding overflows, and the draws depend on the wrap."""
 
     MBIG = 2147483647
     MSEED = 161803398
@@ -127,10 +133,10 @@ class DotNetRandom:
     def __init__(self, seed: Optional[int]):
         if seed is None:
             seed = int.from_bytes(os.urandom(4), "little") & 0x7FFFFFFF
-        seed = int(seed)
+        seed = _i32(int(seed))
         sa = [0] * 56
         sub = self.MBIG if seed == -(2**31) else abs(seed)
-        mj = self.MSEED - sub
+        mj = _i32(self.MSEED - sub)
         sa[55] = mj
         mk = 1
         ii = 0
@@ -139,18 +145,18 @@ class DotNetRandom:
             if ii >= 55:
                 ii -= 55
             sa[ii] = mk
-            mk = mj - mk
+            mk = _i32(mj - mk)
             if mk < 0:
-                mk += self.MBIG
+                mk = _i32(mk + self.MBIG)
             mj = sa[ii]
         for _ in range(1, 5):
             for i in range(1, 56):
                 n = i + 30
                 if n >= 55:
                     n -= 55
-                sa[i] -= sa[1 + n]
+                sa[i] = _i32(sa[i] - sa[1 + n])
                 if sa[i] < 0:
-                    sa[i] += self.MBIG
+                    sa[i] = _i32(sa[i] + self.MBIG)
         self._sa = sa
         self._inext = 0
         self._inextp = 21
@@ -162,11 +168,11 @@ class DotNetRandom:
         b = self._inextp + 1
         if b >= 56:
             b = 1
-        r = self._sa[a] - self._sa[b]
+        r = _i32(self._sa[a] - self._sa[b])
         if r == self.MBIG:
             r -= 1
         if r < 0:
-            r += self.MBIG
+            r = _i32(r + self.MBIG)
         self._sa[a] = r
         self._inext, self._inextp = a, b
         return r
