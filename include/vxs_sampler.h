@@ -46,6 +46,12 @@ extern "C" {
  * least 1024 rows with vocab <= 3072, else one workgroup per row). Results are identical. */
 #define VXS_FLAG_PATH_BLOCK (1u << 8) /* one 256-thread workgroup per row                      */
 #define VXS_FLAG_PATH_WAVE (1u << 9)  /* one wave per row first, 4 rows per workgroup (vocab <= 3072) */
+/* vxs_sample_batch / vxs_sample_batch_device only: instead of reading `u` (which may be NULL),
+ * each sampled row draws its uniform on the device from its slot's generator (vxs_history_seed):
+ * the talker's new Random(Seed) or the code predictor's new Random(Seed + 1). A greedy row draws
+ * nothing, as Select consumes no NextDouble when DoSample is false (Sampler.cs:37,77). */
+#define VXS_FLAG_RNG_TALKER (1u << 10)
+#define VXS_FLAG_RNG_SUB (1u << 11)
 
 /*
  * Per-row sampling parameters (blittable; 36 bytes, 4-byte aligned).
@@ -158,6 +164,14 @@ VXS_API void vxs_history_destroy(vxs_history* h);
 VXS_API int vxs_history_set(vxs_ctx* ctx, vxs_history* h, int slot, const int32_t* ids, int n);
 /* Copy slot `slot`'s history into ids[0..max_ids) and its length into *n. Synchronous. */
 VXS_API int vxs_history_get(vxs_ctx* ctx, vxs_history* h, int slot, int32_t* ids, int max_ids, int* n);
+/* Seed slot `slot`'s two generators as a sequence's samplers are built (TalkerGenerator.cs:217-218,
+ * :345-346): new Random(seed) for the talker, new Random(seed + 1) for the code predictor, with
+ * .NET's seeded generator (Sampler.cs:21) and C#'s wrapping int arithmetic. A job without a seed
+ * passes one of its own choosing. Synchronous. */
+VXS_API int vxs_history_seed(vxs_ctx* ctx, vxs_history* h, int slot, int32_t seed);
+/* The next n NextDouble() values (Sampler.cs:77) of slot `slot`'s talker (stream 0) or
+ * code-predictor (stream 1) generator, drawn on the device into out[0..n). Synchronous. */
+VXS_API int vxs_history_draw(vxs_ctx* ctx, vxs_history* h, int slot, int stream, int n, double* out);
 
 /*
  * One batched sampling stage over host rows whose histories live in `h`: row r penalises with

@@ -160,3 +160,64 @@ def test_generate_batch_equals_generate(ctx, max_batch):
             assert np.array_equal(a, b), f"job {j} frame {t}: batched {a} vs alone {b}"
     calls, rows, boundary = rec.check_against_oracle()
     print(f"max_batch={max_batch}: {calls} batched calls, {rows} rows vs oracle, {boundary} boundary rows", flush=True)
+
+
+def _i32(x):
+    return ((x + 0x80000000) & 0xFFFFFFFF) - 0x80000000
+
+
+def test_device_generators_match_dotnet_random(ctx):
+    """The slot generators drawn on the device reproduce DotNetRandom (the host restatement of .NET's
+    seeded System.Random) bit for bit, for new Random(seed) and new Random(seed + 1)."""
+    from voxwerk_amd.sampler import DotNetRandom
+
+    seeds = [0, 1, 42, 161803399, 10**9, 2**31 - 1, -(2**31), -7, 2_000_000_000, 123456789]
+    with ctx.history(len(seeds), 4) as store:
+        for s, seed in enumerate(seeds):
+            store.seed(s, seed)
+        for s, seed in enumerate(seeds):
+            for stream, sd in (("talker", seed), ("sub", _i32(seed + 1))):
+                host = DotNetRandom(sd)
+                want = np.array([host.NextDouble() for _ in range(700)])
+                got = np.concatenate([store.draw(s, stream, 200), store.draw(s, stream, 500)])
+                assert np.array_equal(got.view(np.uint64), want.view(np.uint64)), (seed, stream)
+
+
+def test_batch_draws_uniforms_on_device(ctx):
+    from voxwerk_amd.sampler import DotNetRandom
+
+    rng = np.random.default_rng(5)
+    rows, vocab = 16, 3072
+    params = _talker_rows(rows, vocab, rng)
+    seeds = rng.integers(-2**31, 2**31, rows).tolist()
+    slots = np.arange(rows, dtype=np.int32)[::-1].copy()
+    host = [DotNetRandom(int(sd)) for sd in seeds]
+    with ctx.history(rows, 16) as a, ctx.history(rows, 16) as b:
+        for r in range(rows):
+            b.seed(int(slots[r]), int(seeds[r]))
+        with pytest.raises(SamplerError):
+            ctx.sample_batch(a, np.zeros((rows, vocab), np.float32), slots, params, None, rng="talker")  # unseeded
+        for t in range(6):
+            x = (rng.standard_normal((rows, vocab)) * 3).astype(np.float32)
+            u = np.array([host[r].NextDouble() if params["do_sample"][r] else 0.0 for r in range(rows)])
+            want = ctx.sample_batch(a, x, slots, params, u)
+            got = ctx.sample_batch(b, x, slots, params, None, rng="talker")
+            assert np.array_equal(got, want), f"step {t}"
+        for r in range(rows):  # greedy rows drew nothing
+            nxt = b.draw(int(slots[r]), "talker", 3)
+            assert nxt.tolist() == [host[r].NextDouble() for _ in range(3)], r
+
+
+@pytest.mark.parametrize("max_batch", [2, 5])
+def test_generate_batch_with_device_generators(ctx, max_batch):
+    jobs = _jobs()
+    model = SyntheticTalker(seed=9)
+    done = {}
+    generate_batch(jobs, max_batch, lambda j, f: done.__setitem__(j, f), model, context=ctx, device_rng=True)
+    for j, job in enumerate(jobs):
+        if job.Options.Seed is None and job.Options.Talker.DoSample:
+            continue  # unseeded sampling: no fixed answer
+        alone = generate(j, job.Options, model, context=ctx)
+        assert len(done[j]) == len(alone), f"job {j}"
+        for t, (a, b) in enumerate(zip(done[j], alone)):
+            assert np.array_equal(a, b), f"job {j} frame {t}: device generators {a} vs host {b}"

@@ -29,6 +29,8 @@ VXS_ERR_NO_DEVICE = -6
 VXS_ERR_HISTORY_FULL = -7
 VXS_FLAG_PATH_BLOCK = 1 << 8
 VXS_FLAG_PATH_WAVE = 1 << 9
+VXS_FLAG_RNG_TALKER = 1 << 10
+VXS_FLAG_RNG_SUB = 1 << 11
 
 
 class VxsParams(ctypes.Structure):
@@ -95,6 +97,8 @@ _SIGNATURES = {
     "vxs_history_destroy": (None, [c_void_p]),
     "vxs_history_set": (c_int, [c_void_p, c_void_p, c_int, _P, c_int]),
     "vxs_history_get": (c_int, [c_void_p, c_void_p, c_int, _P, c_int, POINTER(c_int)]),
+    "vxs_history_seed": (c_int, [c_void_p, c_void_p, c_int, c_int32]),
+    "vxs_history_draw": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, _P]),
     "vxs_sample_batch": (c_int, [c_void_p, c_void_p, c_int, c_int, _P, c_int64, _P, c_int, _P, c_int, _P, _P,
                                  c_uint32]),
     "vxs_sample_batch_device": (c_int, [c_void_p, c_void_p, c_int, c_int, _P, c_int64, _P, c_int, _P, c_int, _P,

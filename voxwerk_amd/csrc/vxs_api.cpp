@@ -83,6 +83,7 @@ struct vxs_ctx {
     std::string err;
     DevBuf d_in, d_ids, d_logits_out, d_probs_out;
     DevBuf d_defer;  // deferral list of the one-wave path: 2 counters, then one entry per row
+    DevBuf d_draw;   // uniforms drawn on the device for a batch call (and vxs_history_draw)
     size_t defer_rows = 0;
     int defer_phase = 0;  // which counter the next call uses
     HostBuf h_in, h_ids, h_out;  // h_in is coherent: polled calls' kernels read it in place
@@ -102,6 +103,8 @@ struct vxs_history {
     int cap = 0;
     int32_t* ids = nullptr;  // [slots][cap]
     int32_t* len = nullptr;  // [slots]
+    int32_t* rng = nullptr;  // [slots][2][kRngWords]: talker and code-predictor generators
+    std::vector<uint8_t> seeded;  // host record of vxs_history_seed per slot
 };
 
 namespace {
@@ -252,8 +255,47 @@ struct ResidentCall {
     const vxs_history* store = nullptr;
     const int32_t* slots = nullptr;
     int append = 0;
+    int rng_stream = -1;  // 0 / 1: draw the uniforms from the slots' talker / code-predictor generators
     const vxs::SampleArgs* done = nullptr;
 };
+
+constexpr uint32_t kRngFlags = VXS_FLAG_RNG_TALKER | VXS_FLAG_RNG_SUB;
+
+int rng_stream_of(uint32_t flags) {
+    return (flags & VXS_FLAG_RNG_TALKER) ? 0 : (flags & VXS_FLAG_RNG_SUB) ? 1 : -1;
+}
+
+// new Random(seed) of .NET (the seeded, legacy subtractive generator), into st[0..kRngWords):
+// SeedArray[1..55], then inext = 0 and inextp = 21. Every step wraps to 32 bits, as C#'s unchecked
+// int arithmetic does (seeds above 161803398 overflow during seeding).
+void dotnet_seed(int32_t seed, int32_t* st) {
+    constexpr int32_t kMbig = 0x7FFFFFFF, kMseed = 161803398;
+    auto sub = [](int32_t a, int32_t b) { return (int32_t)((uint32_t)a - (uint32_t)b); };
+    auto add = [](int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); };
+    for (int i = 0; i < vxs::kRngWords; i++) st[i] = 0;
+    const int32_t subtraction = seed == INT32_MIN ? kMbig : (seed < 0 ? -seed : seed);
+    int32_t mj = sub(kMseed, subtraction);
+    st[55] = mj;
+    int32_t mk = 1;
+    int ii = 0;
+    for (int i = 1; i < 55; i++) {
+        ii += 21;
+        if (ii >= 55) ii -= 55;
+        st[ii] = mk;
+        mk = sub(mj, mk);
+        if (mk < 0) mk = add(mk, kMbig);
+        mj = st[ii];
+    }
+    for (int k = 1; k < 5; k++)
+        for (int i = 1; i < 56; i++) {
+            int n = i + 30;
+            if (n >= 55) n -= 55;
+            st[i] = sub(st[i], st[1 + n]);
+            if (st[i] < 0) st[i] = add(st[i], kMbig);
+        }
+    st[56] = 0;
+    st[57] = 21;
+}
 
 // Row histories of a resident call, and the append kernel that follows its sampler.
 void set_resident(vxs::SampleArgs& a, const vxs_history* h, const int32_t* d_slots) {
@@ -276,6 +318,24 @@ vxs::AppendArgs append_args(const vxs::SampleArgs& a, const vxs_history* h, int 
     b.ids = h->ids;
     b.out_ids = a.out_ids;
     return b;
+}
+
+// Queue the draw of one uniform per sampled row from its slot's generator into ctx->d_draw, and
+// point the sampler's uniforms there.
+hipError_t draw_for(vxs_ctx* ctx, vxs::SampleArgs& a, const vxs_history* h, int stream) {
+    hipError_t e = ctx->d_draw.reserve(sizeof(double) * (size_t)a.rows);
+    if (e != hipSuccess) return e;
+    vxs::DrawArgs b{};
+    b.rows = a.rows;
+    b.slots = h->slots;
+    b.stream = stream;
+    b.slot = a.hist_slot;
+    b.params = a.params;
+    b.params_stride = a.params_stride;
+    b.rng = h->rng;
+    b.u = static_cast<double*>(ctx->d_draw.p);
+    a.u = b.u;
+    return vxs::launch_draw_uniforms(b, ctx->stream);
 }
 
 // Stage inputs and launch. On success the kernels are queued on ctx->stream.
@@ -341,6 +401,7 @@ int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int
         a.done_seq = done->done_seq;
     }
     if (res) set_resident(a, res->store, reinterpret_cast<const int32_t*>(d + L.hoff));
+    if (res && res->rng_stream >= 0) VXS_HIP(ctx, draw_for(ctx, a, res->store, res->rng_stream));
     if (a.path == vxs::kPathQuad) VXS_HIP(ctx, ensure_defer(ctx, rows, a));
     VXS_HIP(ctx, launch_checked(ctx, a));
     if (res) {
@@ -400,6 +461,13 @@ int wait_done(vxs_ctx* ctx, int32_t seq) {
             break;
         }
     }
+    return VXS_OK;
+}
+
+int check_batch_flags(vxs_ctx* ctx, uint32_t flags) {
+    if (flags & ~(kPathFlags | kRngFlags)) return fail(ctx, VXS_ERR_INVALID_ARG, "unknown flags");
+    if ((flags & kPathFlags) == kPathFlags) return fail(ctx, VXS_ERR_INVALID_ARG, "both path flags set");
+    if ((flags & kRngFlags) == kRngFlags) return fail(ctx, VXS_ERR_INVALID_ARG, "both generator flags set");
     return VXS_OK;
 }
 
@@ -480,6 +548,7 @@ VXS_API void vxs_destroy(vxs_ctx* ctx) {
     ctx->d_in.release();
     ctx->d_ids.release();
     ctx->d_defer.release();
+    ctx->d_draw.release();
     ctx->d_done.release();
     ctx->h_done.release();
     ctx->d_logits_out.release();
@@ -653,9 +722,13 @@ VXS_API int vxs_history_create(vxs_ctx* ctx, int slots, int cap, vxs_history** o
         h->device = ctx->device;
         h->slots = slots;
         h->cap = cap;
+        h->seeded.assign((size_t)slots, 0);
+        const size_t rng_bytes = sizeof(int32_t) * (size_t)slots * 2 * vxs::kRngWords;
         hipError_t e = hipMalloc(&h->ids, sizeof(int32_t) * (size_t)slots * (size_t)cap);
         if (e == hipSuccess) e = hipMalloc(&h->len, sizeof(int32_t) * (size_t)slots);
+        if (e == hipSuccess) e = hipMalloc(&h->rng, rng_bytes);
         if (e == hipSuccess) e = hipMemsetAsync(h->len, 0, sizeof(int32_t) * (size_t)slots, ctx->stream);
+        if (e == hipSuccess) e = hipMemsetAsync(h->rng, 0, rng_bytes, ctx->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
         if (e != hipSuccess) {
             vxs_history_destroy(h);
@@ -674,6 +747,7 @@ VXS_API void vxs_history_destroy(vxs_history* h) {
     (void)hipSetDevice(h->device);
     if (h->ids) (void)hipFree(h->ids);
     if (h->len) (void)hipFree(h->len);
+    if (h->rng) (void)hipFree(h->rng);
     delete h;
 }
 
@@ -724,22 +798,72 @@ VXS_API int vxs_history_get(vxs_ctx* ctx, vxs_history* h, int slot, int32_t* ids
     }
 }
 
+VXS_API int vxs_history_seed(vxs_ctx* ctx, vxs_history* h, int slot, int32_t seed) {
+    try {
+        if (!ctx) return VXS_ERR_INVALID_ARG;
+        int rc = check_store(ctx, h);
+        if (rc != VXS_OK) return rc;
+        if ((unsigned)slot >= (unsigned)h->slots) return fail(ctx, VXS_ERR_INVALID_ARG, "slot outside the store");
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        VXS_HIP(ctx, ctx->h_ids.reserve(sizeof(int32_t) * 2 * vxs::kRngWords));
+        int32_t* st = static_cast<int32_t*>(ctx->h_ids.p);
+        dotnet_seed(seed, st);
+        dotnet_seed((int32_t)((uint32_t)seed + 1u), st + vxs::kRngWords);  // Seed + 1, unchecked
+        VXS_HIP(ctx, hipMemcpyAsync(h->rng + (int64_t)slot * 2 * vxs::kRngWords, st, sizeof(int32_t) * 2 * vxs::kRngWords,
+                                    hipMemcpyHostToDevice, ctx->stream));
+        VXS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        h->seeded[slot] = 1;
+        ctx->err.clear();
+        return VXS_OK;
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
+VXS_API int vxs_history_draw(vxs_ctx* ctx, vxs_history* h, int slot, int stream, int n, double* out) {
+    try {
+        if (!ctx) return VXS_ERR_INVALID_ARG;
+        int rc = check_store(ctx, h);
+        if (rc != VXS_OK) return rc;
+        if ((unsigned)slot >= (unsigned)h->slots) return fail(ctx, VXS_ERR_INVALID_ARG, "slot outside the store");
+        if (stream != 0 && stream != 1) return fail(ctx, VXS_ERR_INVALID_ARG, "stream must be 0 or 1");
+        if (n < 0 || (n > 0 && !out)) return fail(ctx, VXS_ERR_INVALID_ARG, "bad n / out");
+        if (!h->seeded[slot]) return fail(ctx, VXS_ERR_INVALID_ARG, "slot's generators are not seeded");
+        if (n == 0) return VXS_OK;
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        VXS_HIP(ctx, ctx->d_draw.reserve(sizeof(double) * (size_t)n));
+        VXS_HIP(ctx, vxs::launch_draw_sequence(h->rng + ((int64_t)slot * 2 + stream) * vxs::kRngWords, n,
+                                               static_cast<double*>(ctx->d_draw.p), ctx->stream));
+        if ((rc = fetch(ctx, out, ctx->d_draw.p, sizeof(double) * (size_t)n)) != VXS_OK) return rc;
+        ctx->err.clear();
+        return VXS_OK;
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
 VXS_API int vxs_sample_batch(vxs_ctx* ctx, vxs_history* h, int rows, int vocab, const float* logits, int64_t ld,
                              const int32_t* slots, int append, const vxs_params* params, int params_stride,
                              const double* u, int32_t* out_ids, uint32_t flags) {
     try {
         int rc = check_shape(ctx, rows, vocab, logits, ld, params, params_stride, out_ids);
         if (rc != VXS_OK) return rc;
-        if ((rc = check_flags(ctx, flags)) != VXS_OK) return rc;
+        if ((rc = check_batch_flags(ctx, flags)) != VXS_OK) return rc;
         if ((rc = check_store(ctx, h)) != VXS_OK) return rc;
         if (rows == 0) return VXS_OK;
-        if ((rc = check_params_host(ctx, rows, params, params_stride, u)) != VXS_OK) return rc;
+        const int stream = rng_stream_of(flags);
+        if (stream < 0 && (rc = check_params_host(ctx, rows, params, params_stride, u)) != VXS_OK) return rc;
         if ((rc = check_slots_host(ctx, h, rows, slots)) != VXS_OK) return rc;
+        if (stream >= 0)
+            for (int r = 0; r < rows; r++)
+                if (!h->seeded[slots[r]])
+                    return fail(ctx, VXS_ERR_INVALID_ARG, "row " + std::to_string(r) + ": slot's generators are not seeded");
         VXS_HIP(ctx, hipSetDevice(ctx->device));
         ResidentCall res;
         res.store = h;
         res.slots = slots;
         res.append = append != 0;
+        res.rng_stream = stream;
         if (polled_call(rows, vocab, flags, false, false)) {
             vxs::SampleArgs done{};
             VXS_HIP(ctx, ensure_done(ctx, rows, done));
@@ -774,7 +898,7 @@ VXS_API int vxs_sample_batch_device(vxs_ctx* ctx, vxs_history* h, int rows, int 
     try {
         int rc = check_shape(ctx, rows, vocab, d_logits, ld, d_params, params_stride, d_out_ids);
         if (rc != VXS_OK) return rc;
-        if ((rc = check_flags(ctx, flags)) != VXS_OK) return rc;
+        if ((rc = check_batch_flags(ctx, flags)) != VXS_OK) return rc;
         if ((rc = check_store(ctx, h)) != VXS_OK) return rc;
         if (rows == 0) return VXS_OK;
         if (!d_slots) return fail(ctx, VXS_ERR_INVALID_ARG, "slots is NULL");
@@ -792,6 +916,7 @@ VXS_API int vxs_sample_batch_device(vxs_ctx* ctx, vxs_history* h, int rows, int 
         a.out_ids = d_out_ids;
         a.kflags = 0;
         a.path = choose_path(flags, rows, vocab);
+        if (rng_stream_of(flags) >= 0) VXS_HIP(ctx, draw_for(ctx, a, h, rng_stream_of(flags)));
         if (a.path == vxs::kPathQuad) VXS_HIP(ctx, ensure_defer(ctx, rows, a));
         VXS_HIP(ctx, launch_checked(ctx, a));
         VXS_HIP(ctx, vxs::launch_history_append(append_args(a, h, append != 0), ctx->stream));

@@ -5,6 +5,8 @@
 // draw (:369) and grown by one id after it (:374). Here the histories stay in device memory, one
 // fixed-capacity slot per sequence ([slots][cap] ids plus [slots] lengths), and this kernel runs
 // after the sampler to append each row's id to its slot, so no history crosses PCIe per step.
+// A slot also holds its sequence's two generators, new Random(seed) for the talker and
+// new Random(seed + 1) for the code predictor (:345-346), so the uniforms can be drawn here too.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -41,7 +43,52 @@ __global__ __launch_bounds__(kAT) void history_append_kernel(AppendArgs a) {
     }
 }
 
+// One NextDouble() of a .NET seeded Random (InternalSample() * (1.0 / int.MaxValue)) with C#'s
+// wrapping int arithmetic; advances the state in place.
+__device__ __forceinline__ double next_double(int32_t* st) {
+    constexpr int32_t kMbig = 0x7FFFFFFF;
+    int i = st[56] + 1;
+    if (i >= 56) i = 1;
+    int j = st[57] + 1;
+    if (j >= 56) j = 1;
+    int32_t v = (int32_t)((uint32_t)st[i] - (uint32_t)st[j]);
+    if (v == kMbig) v--;
+    if (v < 0) v = (int32_t)((uint32_t)v + (uint32_t)kMbig);
+    st[i] = v;
+    st[56] = i;
+    st[57] = j;
+    return (double)v * (1.0 / 2147483647.0);
+}
+
+__global__ __launch_bounds__(kAT) void draw_uniforms_kernel(DrawArgs a) {
+    for (int r = blockIdx.x * kAT + threadIdx.x; r < a.rows; r += gridDim.x * kAT) {
+        const int s = a.slot[r];
+        const int sampled = a.params[(int64_t)r * a.params_stride].do_sample;
+        double u = 0.0;
+        if (sampled && (unsigned)s < (unsigned)a.slots) u = next_double(a.rng + ((int64_t)s * 2 + a.stream) * kRngWords);
+        a.u[r] = u;
+    }
+}
+
+__global__ void draw_sequence_kernel(int32_t* st, int n, double* out) {
+    if (threadIdx.x == 0)
+        for (int k = 0; k < n; k++) out[k] = next_double(st);
+}
+
 }  // namespace
+
+hipError_t launch_draw_uniforms(const DrawArgs& a, hipStream_t stream) {
+    if (a.rows <= 0) return hipSuccess;
+    const int blocks = std::min((a.rows + kAT - 1) / kAT, 1024);
+    hipLaunchKernelGGL(draw_uniforms_kernel, dim3(blocks), dim3(kAT), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_draw_sequence(int32_t* state, int n, double* out, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(draw_sequence_kernel, dim3(1), dim3(64), 0, stream, state, n, out);
+    return hipGetLastError();
+}
 
 hipError_t launch_history_append(const AppendArgs& a, hipStream_t stream) {
     if (a.rows <= 0) return hipSuccess;

@@ -98,9 +98,31 @@ struct AppendArgs {
     int32_t done_seq;
 };
 
+// Per-sequence generators of a resident store: .NET's seeded System.Random state, kRngWords int32
+// per generator (SeedArray[1..55] at [1..55], inext at [56], inextp at [57]), two per slot (the
+// talker's at 2s, the code predictor's at 2s + 1).
+constexpr int kRngWords = 64;
+
+// Uniforms of a batch call drawn on the device: row r takes the next NextDouble() of generator
+// 2 * slot[r] + stream when it samples (params do_sample), else 0 and no draw (Sampler.cs:37,77).
+// A slot outside [0, slots) gets 0 (the append kernel fails the row).
+struct DrawArgs {
+    int rows;
+    int slots;
+    int stream;
+    const int32_t* slot;
+    const vxs_params* params;
+    int params_stride;
+    int32_t* rng;
+    double* u;
+};
+
 // Enqueue the sampler on `stream`. Returns hipSuccess or the launch error.
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream);
 hipError_t launch_sample_wide(const SampleArgs& a, hipStream_t stream);
 hipError_t launch_history_append(const AppendArgs& a, hipStream_t stream);
+hipError_t launch_draw_uniforms(const DrawArgs& a, hipStream_t stream);
+// n successive NextDouble() of one generator into out[0..n) (one thread; a check and debug aid).
+hipError_t launch_draw_sequence(int32_t* state, int n, double* out, hipStream_t stream);
 
 }  // namespace vxs

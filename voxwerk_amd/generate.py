@@ -10,6 +10,7 @@ library: it only has to turn codes into logits.
 """
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass, field
 from typing import Any, Callable, List, Optional, Protocol, Sequence
 
@@ -101,14 +102,16 @@ def generate(job: int, opts: GenerationOptions, model: TalkerModel, context: Opt
 def generate_batch(jobs: Sequence[BatchJob], max_batch: int, on_done: Callable[[int, List[np.ndarray]], None],
                    model: TalkerModel, context: Optional[Context] = None, vocab: int = TALKER_VOCAB,
                    cp_vocab: int = CP_VOCAB, groups: int = NUM_CODE_GROUPS, eos_id: int = CODEC_EOS_ID,
-                   path: str = "auto") -> None:
+                   path: str = "auto", device_rng: bool = False) -> None:
     """``GenerateBatch`` (TalkerGenerator.cs:322-455): up to ``max_batch`` sequences advance in
     lockstep; a finished one is reported through ``on_done(job, frames)`` and its slot refilled from the
     queue. Each job keeps its own ``Sampler(Seed)`` / ``Sampler(Seed + 1)``, so its frames do not
     depend on the batch it ran in.
 
     Per step: one ``vxs_sample_batch`` over the talker rows (penalty from the resident history,
-    suppression, select, on-device ``History.Add``), then one per code-predictor group."""
+    suppression, select, on-device ``History.Add``), then one per code-predictor group. With
+    ``device_rng`` the two generators of each job live in its slot and draw on the GPU (the same
+    .NET sequences, so the same frames); otherwise the host draws them."""
     if max_batch <= 0:
         raise ValueError("max_batch must be positive")
     ctx = context or default_context()
@@ -125,6 +128,8 @@ def generate_batch(jobs: Sequence[BatchJob], max_batch: int, on_done: Callable[[
                 opts = jobs[nxt].Options
                 slot = free.pop()
                 store.set(slot, ())  # a new sequence starts with an empty history
+                if device_rng:
+                    store.seed(slot, opts.Seed if opts.Seed is not None else int.from_bytes(os.urandom(4), "little"))
                 logits = np.array(model.prefill(nxt), dtype=np.float32).reshape(-1)
                 active.append(_Active(nxt, opts, slot, Sampler(opts.Seed, ctx), Sampler(_sub_seed(opts), ctx), logits))
                 nxt += 1
@@ -133,8 +138,12 @@ def generate_batch(jobs: Sequence[BatchJob], max_batch: int, on_done: Callable[[
             A = len(active)
             x = np.stack([a.logits[:vocab] for a in active])
             params = np.stack([talker_params(a.options, a.step, vocab, eos_id) for a in active])
-            u = np.array([a.sampler.NextUniform(a.options.Talker) for a in active])
-            code0 = ctx.sample_batch(store, x, [a.slot for a in active], params, u, append=True, path=path)
+            slots = [a.slot for a in active]
+            if device_rng:
+                code0 = ctx.sample_batch(store, x, slots, params, None, append=True, path=path, rng="talker")
+            else:
+                u = np.array([a.sampler.NextUniform(a.options.Talker) for a in active])
+                code0 = ctx.sample_batch(store, x, slots, params, u, append=True, path=path)
             keep: List[_Active] = []
             first: List[int] = []
             for a, c in zip(active, code0.tolist()):
@@ -158,8 +167,12 @@ def generate_batch(jobs: Sequence[BatchJob], max_batch: int, on_done: Callable[[
                 cp = np.ascontiguousarray(model.code_predictor(job_ids, g, frames), dtype=np.float32)
                 if cp.shape != (A, cp_vocab):
                     raise ValueError(f"code_predictor returned {cp.shape}, expected {(A, cp_vocab)}")
-                u = np.array([a.sub_sampler.NextUniform(a.options.SubTalker) for a in active])
-                frames[:, g] = ctx.sample(cp, sub, u, path=path)
+                if device_rng:  # the code-predictor generators of the slots; no history involved
+                    frames[:, g] = ctx.sample_batch(store, cp, [a.slot for a in active], sub, None, append=False,
+                                                    path=path, rng="sub")
+                else:
+                    u = np.array([a.sub_sampler.NextUniform(a.options.SubTalker) for a in active])
+                    frames[:, g] = ctx.sample(cp, sub, u, path=path)
 
             # 3. one talker step for all sequences                                     :429-448
             steps = [a.step for a in active]

@@ -202,6 +202,7 @@ def _csr(histories: Optional[Iterable[Iterable[int]]], rows: int):
 
 
 PATH_FLAGS = {"auto": 0, "block": _lib.VXS_FLAG_PATH_BLOCK, "wave": _lib.VXS_FLAG_PATH_WAVE}
+RNG_FLAGS = {None: 0, "talker": _lib.VXS_FLAG_RNG_TALKER, "sub": _lib.VXS_FLAG_RNG_SUB}
 
 
 class Context:
@@ -322,9 +323,11 @@ class Context:
 
     def sample_batch(self, store: "HistoryStore", logits: np.ndarray, slots, params: np.ndarray,
                      u: Optional[np.ndarray] = None, append: bool = True, raise_on_error: bool = True,
-                     path: str = "auto") -> np.ndarray:
+                     path: str = "auto", rng: Optional[str] = None) -> np.ndarray:
         """One batched stage over host rows whose histories live in `store`: row r penalises with
-        slot slots[r] and, with `append`, its id is added to that slot (vxs_sample_batch)."""
+        slot slots[r] and, with `append`, its id is added to that slot (vxs_sample_batch). With
+        ``rng="talker"`` or ``"sub"`` the uniforms come from the slots' generators on the device
+        (``store.seed``) and `u` is ignored."""
         logits = np.ascontiguousarray(logits, dtype=np.float32)
         if logits.ndim == 1:
             logits = logits.reshape(1, -1)
@@ -342,18 +345,20 @@ class Context:
                 raise ValueError("u must have one value per row")
         ids = np.empty(rows, dtype=np.int32)
         rc = self._lib.vxs_sample_batch(self._h, store.handle, rows, vocab, ptr(logits), vocab, ptr(slots),
-                                        1 if append else 0, ptr(params), stride, ptr(u), ptr(ids), PATH_FLAGS[path])
+                                        1 if append else 0, ptr(params), stride, ptr(u), ptr(ids),
+                                        PATH_FLAGS[path] | RNG_FLAGS[rng])
         if rc != 0 and (raise_on_error or rc not in (_lib.VXS_ERR_ID_OUT_OF_RANGE, _lib.VXS_ERR_NONFINITE,
                                                      _lib.VXS_ERR_HISTORY_FULL)):
             _raise(rc, self.last_error())
         return ids
 
     def sample_batch_device(self, store: "HistoryStore", rows: int, vocab: int, logits, ld: int, slots, params,
-                            params_stride: int, u, out_ids, append: bool = True, path: str = "auto") -> None:
+                            params_stride: int, u, out_ids, append: bool = True, path: str = "auto",
+                            rng: Optional[str] = None) -> None:
         """vxs_sample_batch_device: device pointers (torch tensors or ints), asynchronous."""
         rc = self._lib.vxs_sample_batch_device(self._h, store.handle, rows, vocab, ptr(logits), ld, ptr(slots),
                                                1 if append else 0, ptr(params), params_stride, ptr(u),
-                                               ptr(out_ids), PATH_FLAGS[path])
+                                               ptr(out_ids), PATH_FLAGS[path] | RNG_FLAGS[rng])
         self._check(rc)
 
 
@@ -380,6 +385,19 @@ class HistoryStore:
         a = np.ascontiguousarray(list(ids), dtype=np.int32)
         self._ctx._check(self._lib.vxs_history_set(self._ctx.handle, self._h, slot, ptr(a) if a.size else None,
                                                    int(a.size)))
+
+    def seed(self, slot: int, seed: int) -> None:
+        """Seed the slot's generators: new Random(seed) (talker) and new Random(seed + 1) (code
+        predictor), as a sequence's samplers are built (TalkerGenerator.cs:345-346)."""
+        s32 = ((int(seed) + 0x80000000) & 0xFFFFFFFF) - 0x80000000
+        self._ctx._check(self._lib.vxs_history_seed(self._ctx.handle, self._h, slot, s32))
+
+    def draw(self, slot: int, stream: str, n: int) -> np.ndarray:
+        """The next n NextDouble() of the slot's "talker" or "sub" generator, drawn on the device."""
+        out = np.empty(n, dtype=np.float64)
+        self._ctx._check(self._lib.vxs_history_draw(self._ctx.handle, self._h, slot, {"talker": 0, "sub": 1}[stream],
+                                                    n, ptr(out) if n else None))
+        return out
 
     def get(self, slot: int) -> np.ndarray:
         n = ctypes.c_int(0)
