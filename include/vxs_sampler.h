@@ -198,6 +198,33 @@ VXS_API int vxs_sample_batch_device(vxs_ctx* ctx, vxs_history* h, int rows, int 
                                     int append, const vxs_params* d_params, int params_stride,
                                     const double* d_u, int32_t* d_out_ids, uint32_t flags);
 
+/*
+ * Embedding rows of sampled ids, the step after the sampler, so that ids need not return to the
+ * host between sampling and the next forward pass. Tables are bf16 [vocab][hidden], widened to
+ * fp32 exactly (Bf16.ToFloat, src/Voxwerk/Numerics/Bf16.cs:13); sums run in the reference's order,
+ * so rows are bit-identical. Device pointers, asynchronous on the context stream. status[r] gets 0,
+ * or VXS_ERR_ID_OUT_OF_RANGE for a row holding an id outside its table, which is then not written
+ * (the reference throws ArgumentOutOfRangeException, TalkerModel.cs:102,109).
+ *
+ * vxs_embed_device replaces CodecEmbedding / CodePredictorEmbedding (TalkerModel.cs:100-111):
+ * out[r] = table[ids[r]] (add = 0) or out[r] += table[ids[r]] (add = 1), as called at
+ * TalkerGenerator.cs:258, :271, :411 and :422.
+ */
+VXS_API int vxs_embed_device(vxs_ctx* ctx, int rows, int hidden, const int32_t* d_ids, const uint16_t* d_table,
+                             int vocab, float* d_out, int64_t ld_out, int add, int32_t* d_status);
+
+/*
+ * FrameEmbedding (TalkerModel.cs:113-117) for `rows` frames, plus the talker step's text row
+ * (TalkerGenerator.cs:280-283, :435-439): out[r] = E0[codes[r][0]] + E1[codes[r][1]] + ... +
+ * E_{groups-1}[codes[r][groups-1]] (+ addend[r] when d_addend is not NULL), left to right in fp32.
+ * E0 = d_codec_table [vocab][hidden]; E_g = d_cp_tables + (g-1) * cp_vocab * hidden, g >= 1, the
+ * code predictor's tables stored back to back. codes [rows][ld_codes] int32.
+ */
+VXS_API int vxs_frame_embed_device(vxs_ctx* ctx, int rows, int groups, int hidden, const int32_t* d_codes,
+                                   int64_t ld_codes, const uint16_t* d_codec_table, int vocab,
+                                   const uint16_t* d_cp_tables, int cp_vocab, const float* d_addend,
+                                   int64_t ld_addend, float* d_out, int64_t ld_out, int32_t* d_status);
+
 #ifdef __cplusplus
 }
 #endif

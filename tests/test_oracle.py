@@ -390,3 +390,38 @@ def test_planted_mistake_is_caught():
     o = run1(x, P(temperature=0.9), want_logits=True)
     assert np.array_equal(o["logits"][0], x * inv)
     assert not np.array_equal(o["logits"][0], (x / F32(0.9)).astype(F32))
+
+
+# ---------------------------------------------------------------------------------------------
+# Embedding lookups of sampled ids (oracle/embedding_np.py)
+# ---------------------------------------------------------------------------------------------
+def test_embedding_widen_special_encodings():
+    from oracle.embedding_np import widen
+
+    got = widen(np.array([0x3F80, 0xC000, 0x7F80, 0xFF80, 0x0001, 0x8000, 0x4B80], np.uint16))
+    assert got[0] == 1.0 and got[1] == -2.0
+    assert np.isposinf(got[2]) and np.isneginf(got[3])
+    assert got[4] == math.ldexp(1.0, -133)  # smallest bf16 subnormal: 2^-126 * 2^-7
+    assert got[5] == 0.0 and math.copysign(1.0, float(got[5])) == -1.0
+    assert got[6] == 2.0**24
+
+
+def test_frame_embed_order_and_precision():
+    """2^24 + 1 + 1 is 2^24 left to right in fp32 (each +1 ties to even), 2^24 + 2 in any other
+    grouping or in fp64; (1 + 1) + 2^24 with the text row last is 2^24 + 2, 2^24 if it came first."""
+    from oracle.embedding_np import embed, frame_embed
+
+    codec = np.array([[0x4B80, 0x3F80]], np.uint16)  # row 0: [2^24, 1]
+    cp = np.array([[[0x3F80, 0x3F80]], [[0x3F80, 0x0000]]], np.uint16)  # two code-predictor tables, 1 row each
+    out, st = frame_embed(np.array([[0, 0, 0]]), codec, cp)
+    assert st.tolist() == [0]
+    assert out[0, 0] == 2.0**24 and out[0, 1] == 2.0
+    out, _ = frame_embed(np.array([[0, 0]]), np.array([[0x3F80, 0x3F80]], np.uint16), cp[:1],
+                         addend=np.array([[2.0**24, 0.0]], np.float32))
+    assert out[0, 0] == 2.0**24 + 2 and out[0, 1] == 2.0
+    prev = np.full((2, 2), 7.0, np.float32)
+    out, st = frame_embed(np.array([[0, 0, 1], [1, 0, 0]]), codec, cp, out=prev.copy())
+    assert st.tolist() == [-2, -2] and np.all(out == 7.0)  # bad ids: rows untouched
+    o = np.full((2, 2), 2.0**24, np.float32)
+    st = embed([0, 5], np.array([[0x3F80, 0x4000]], np.uint16), o, add=True)
+    assert st.tolist() == [0, -2] and o[0].tolist() == [2.0**24, 2.0**24 + 2] and o[1, 0] == 2.0**24

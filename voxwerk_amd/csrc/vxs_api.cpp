@@ -927,4 +927,72 @@ VXS_API int vxs_sample_batch_device(vxs_ctx* ctx, vxs_history* h, int rows, int 
     }
 }
 
+VXS_API int vxs_embed_device(vxs_ctx* ctx, int rows, int hidden, const int32_t* d_ids, const uint16_t* d_table,
+                             int vocab, float* d_out, int64_t ld_out, int add, int32_t* d_status) {
+    try {
+        if (!ctx) return VXS_ERR_INVALID_ARG;
+        if (rows < 0 || hidden <= 0 || vocab <= 0 || ld_out < hidden)
+            return fail(ctx, VXS_ERR_INVALID_ARG, "bad rows, hidden, vocab or ld_out");
+        if (rows == 0) return VXS_OK;
+        if (!d_ids || !d_table || !d_out || !d_status) return fail(ctx, VXS_ERR_INVALID_ARG, "null pointer");
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        vxs::EmbedArgs a{};
+        a.rows = rows;
+        a.hidden = hidden;
+        a.vocab = vocab;
+        a.add = add != 0;
+        a.vec = hidden % 4 == 0 && ld_out % 4 == 0 && ((uintptr_t)d_table & 7u) == 0 && ((uintptr_t)d_out & 15u) == 0;
+        a.ids = d_ids;
+        a.table = d_table;
+        a.out = d_out;
+        a.ld_out = ld_out;
+        a.status = d_status;
+        VXS_HIP(ctx, vxs::launch_embed(a, ctx->stream));
+        ctx->err.clear();
+        return VXS_OK;
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
+VXS_API int vxs_frame_embed_device(vxs_ctx* ctx, int rows, int groups, int hidden, const int32_t* d_codes,
+                                   int64_t ld_codes, const uint16_t* d_codec_table, int vocab,
+                                   const uint16_t* d_cp_tables, int cp_vocab, const float* d_addend,
+                                   int64_t ld_addend, float* d_out, int64_t ld_out, int32_t* d_status) {
+    try {
+        if (!ctx) return VXS_ERR_INVALID_ARG;
+        if (rows < 0 || groups < 1 || hidden <= 0 || vocab <= 0 || ld_codes < groups || ld_out < hidden)
+            return fail(ctx, VXS_ERR_INVALID_ARG, "bad rows, groups, hidden, vocab, ld_codes or ld_out");
+        if (groups > 1 && (cp_vocab <= 0 || !d_cp_tables))
+            return fail(ctx, VXS_ERR_INVALID_ARG, "code predictor tables missing");
+        if (d_addend && ld_addend < hidden) return fail(ctx, VXS_ERR_INVALID_ARG, "ld_addend < hidden");
+        if (rows == 0) return VXS_OK;
+        if (!d_codes || !d_codec_table || !d_out || !d_status) return fail(ctx, VXS_ERR_INVALID_ARG, "null pointer");
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        vxs::FrameEmbedArgs a{};
+        a.rows = rows;
+        a.groups = groups;
+        a.hidden = hidden;
+        a.vocab = vocab;
+        a.cp_vocab = cp_vocab;
+        a.vec = hidden % 4 == 0 && ld_out % 4 == 0 && ((uintptr_t)d_codec_table & 7u) == 0 &&
+                ((uintptr_t)d_cp_tables & 7u) == 0 && ((uintptr_t)d_out & 15u) == 0 &&
+                (!d_addend || (ld_addend % 4 == 0 && ((uintptr_t)d_addend & 15u) == 0));
+        a.codes = d_codes;
+        a.ld_codes = ld_codes;
+        a.codec_table = d_codec_table;
+        a.cp_tables = d_cp_tables;
+        a.addend = d_addend;
+        a.ld_addend = ld_addend;
+        a.out = d_out;
+        a.ld_out = ld_out;
+        a.status = d_status;
+        VXS_HIP(ctx, vxs::launch_frame_embed(a, ctx->stream));
+        ctx->err.clear();
+        return VXS_OK;
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
 }  // extern "C"

@@ -117,6 +117,32 @@ struct DrawArgs {
     double* u;
 };
 
+// Embedding of sampled ids (vxs_embed.hip). `vec`: hidden % 4 == 0 and every base pointer and
+// leading dimension allows 8-byte bf16 and 16-byte fp32 accesses. status[r] = 0 or
+// VXS_ERR_ID_OUT_OF_RANGE (the row is then not written).
+struct EmbedArgs {
+    int rows, hidden, vocab, add, vec;
+    const int32_t* ids;
+    const uint16_t* table;  // [vocab][hidden] bf16
+    float* out;             // [rows][ld_out]
+    int64_t ld_out;
+    int32_t* status;
+};
+struct FrameEmbedArgs {
+    int rows, groups, hidden, vocab, cp_vocab, vec;
+    const int32_t* codes;  // [rows][ld_codes]
+    int64_t ld_codes;
+    const uint16_t* codec_table;  // [vocab][hidden] bf16: codebook 0
+    const uint16_t* cp_tables;    // [groups - 1][cp_vocab][hidden] bf16: codebooks 1..groups-1
+    const float* addend;          // optional [rows][ld_addend], added last
+    int64_t ld_addend;
+    float* out;
+    int64_t ld_out;
+    int32_t* status;
+};
+hipError_t launch_embed(const EmbedArgs& a, hipStream_t stream);
+hipError_t launch_frame_embed(const FrameEmbedArgs& a, hipStream_t stream);
+
 // Enqueue the sampler on `stream`. Returns hipSuccess or the launch error.
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream);
 hipError_t launch_sample_wide(const SampleArgs& a, hipStream_t stream);

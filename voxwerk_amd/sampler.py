@@ -361,6 +361,19 @@ class Context:
                                                ptr(out_ids), PATH_FLAGS[path] | RNG_FLAGS[rng])
         self._check(rc)
 
+    # embedding lookups of sampled ids (device pointers, asynchronous) ------------------------------
+    def embed_device(self, rows: int, hidden: int, ids, table, vocab: int, out, ld_out: int, add: bool, status) -> None:
+        """vxs_embed_device: out[r] = table[ids[r]] or += it (CodecEmbedding / CodePredictorEmbedding)."""
+        self._check(self._lib.vxs_embed_device(self._h, rows, hidden, ptr(ids), ptr(table), vocab, ptr(out), ld_out,
+                                               1 if add else 0, ptr(status)))
+
+    def frame_embed_device(self, rows: int, groups: int, hidden: int, codes, ld_codes: int, codec_table, vocab: int,
+                           cp_tables, cp_vocab: int, out, ld_out: int, status, addend=None, ld_addend: int = 0) -> None:
+        """vxs_frame_embed_device: FrameEmbedding of `rows` frames (+ the text row `addend`)."""
+        self._check(self._lib.vxs_frame_embed_device(self._h, rows, groups, hidden, ptr(codes), ld_codes,
+                                                     ptr(codec_table), vocab, ptr(cp_tables), cp_vocab, ptr(addend),
+                                                     ld_addend, ptr(out), ld_out, ptr(status)))
+
 
 class HistoryStore:
     """Device-resident histories (vxs_history): ``slots`` sequences of at most ``cap`` ids each, all
