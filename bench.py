@@ -96,6 +96,43 @@ def native_frame(rows, iters, serial=False):
     return json.loads(p.stdout.strip().splitlines()[-1])
 
 
+def measure_frame_embedding(ctx, rows: int, steps: int, hip, np) -> dict:
+    """vxs_frame_embed_device over `rows` frames (16 codebooks, hidden 1024, talker and code-predictor
+    tables of the real shapes, random bf16 contents, a text row added): HIP events on the context
+    stream. Algorithmic bytes per row: 16 table rows of 2 KiB, the text row and the output row
+    (4 KiB each), 16 codes and the status."""
+    groups, hidden, vocab, cp_vocab = 16, 1024, 3072, 2048
+    rng = np.random.default_rng(3)
+    codec = rng.integers(0, 0x3F00, (vocab, hidden), dtype=np.uint16)
+    cp = rng.integers(0, 0x3F00, (groups - 1, cp_vocab, hidden), dtype=np.uint16)
+    codes = np.concatenate([rng.integers(0, vocab, (rows, 1)), rng.integers(0, cp_vocab, (rows, groups - 1))], 1)
+    d_codes = hip.DeviceArray.from_numpy(codes.astype(np.int32))
+    d_codec, d_cp = hip.DeviceArray.from_numpy(codec), hip.DeviceArray.from_numpy(cp)
+    d_text = hip.DeviceArray.from_numpy(rng.standard_normal((rows, hidden)).astype(np.float32))
+    d_out, d_st = hip.DeviceArray((rows, hidden), np.float32), hip.DeviceArray((rows,), np.int32)
+
+    def step():
+        ctx.frame_embed_device(rows, groups, hidden, d_codes, groups, d_codec, vocab, d_cp, cp_vocab, d_out, hidden,
+                               d_st, addend=d_text, ld_addend=hidden)
+
+    for _ in range(20):
+        step()
+    hip.synchronize()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(ctx.stream())
+    for _ in range(steps):
+        step()
+    e1.record(ctx.stream())
+    e1.synchronize()
+    us = e0.elapsed_ms(e1) / steps * 1e3
+    per_row = groups * hidden * 2 + 2 * hidden * 4 + groups * 4 + 4
+    gbps = rows * per_row / (us * 1e-6) / 1e9
+    assert not d_st.numpy().any()
+    return {"workload": f"frame_embedding {rows} frames x 16 codebooks x 1024 (+ text row), device-resident",
+            "us_per_step": round(us, 3), "algorithmic_bytes": rows * per_row, "gbps": round(gbps, 1),
+            "pct_of_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2)}
+
+
 def read_traffic():
     """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, or None."""
     try:
@@ -417,6 +454,11 @@ def main() -> int:
             extra["generate_batch_frame"] = m
             log(f"[bench] generate_batch frame ({FRAME_ROWS} sequences): batched p50 {fb['p50_us']:.1f} us "
                 f"({fb['calls_per_frame']} calls), serial p50 {m['serial_us_p50']} us")
+        # embedding of the sampled frames (the step after the sampler)
+        for n_rows, steps_e in ((FRAME_ROWS, 2000), (4096, 500)):
+            m = measure_frame_embedding(ctx, n_rows, steps_e, hip, np)
+            extra[f"frame_embedding_{n_rows}"] = m
+            log(f"[bench] {m['workload']}: {m['us_per_step']:.2f} us/step, {m['gbps']:.0f} GB/s algorithmic")
 
     traffic = read_traffic()
     out = {

@@ -104,6 +104,39 @@ __global__ __launch_bounds__(kET) void frame_embed_kernel(FrameEmbedArgs a) {
     }
 }
 
+// The same for the talker's 16 codebooks with all codes read up front and every table row of a
+// sweep in flight before the sums (the general loop waits on each gather in turn).
+constexpr int kGroups = 16;
+__global__ __launch_bounds__(kET) void frame_embed16_kernel(FrameEmbedArgs a) {
+    const int r = blockIdx.x;
+    const int32_t* codes = a.codes + (int64_t)r * a.ld_codes;
+    int c[kGroups];
+#pragma unroll
+    for (int g = 0; g < kGroups; g++) c[g] = codes[g];
+    bool ok = (unsigned)c[0] < (unsigned)a.vocab;
+#pragma unroll
+    for (int g = 1; g < kGroups; g++) ok = ok && (unsigned)c[g] < (unsigned)a.cp_vocab;
+    if (threadIdx.x == 0) a.status[r] = ok ? 0 : VXS_ERR_ID_OUT_OF_RANGE;
+    if (!ok) return;
+    float* dst = a.out + (int64_t)r * a.ld_out;
+    const float* add = a.addend ? a.addend + (int64_t)r * a.ld_addend : nullptr;
+    const bool vec = a.vec;
+    for (int i = threadIdx.x * 4; i < a.hidden; i += kET * 4) {
+        const int n = a.hidden - i;
+        f4 e[kGroups];
+        e[0] = gather4(a.codec_table + (int64_t)c[0] * a.hidden + i, n, vec);
+#pragma unroll
+        for (int g = 1; g < kGroups; g++)
+            e[g] = gather4(a.cp_tables + ((int64_t)(g - 1) * a.cp_vocab + c[g]) * a.hidden + i, n, vec);
+        const f4 t = add ? load4(add + i, n, vec) : f4{0.f, 0.f, 0.f, 0.f};
+        f4 acc = e[0];
+#pragma unroll
+        for (int g = 1; g < kGroups; g++) acc = acc + e[g];
+        if (add) acc = acc + t;
+        store4(dst + i, acc, n, vec);
+    }
+}
+
 }  // namespace
 
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t stream) {
@@ -114,7 +147,10 @@ hipError_t launch_embed(const EmbedArgs& a, hipStream_t stream) {
 
 hipError_t launch_frame_embed(const FrameEmbedArgs& a, hipStream_t stream) {
     if (a.rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(frame_embed_kernel, dim3(a.rows), dim3(kET), 0, stream, a);
+    if (a.groups == kGroups)
+        hipLaunchKernelGGL(frame_embed16_kernel, dim3(a.rows), dim3(kET), 0, stream, a);
+    else
+        hipLaunchKernelGGL(frame_embed_kernel, dim3(a.rows), dim3(kET), 0, stream, a);
     return hipGetLastError();
 }
 
