@@ -199,6 +199,20 @@ VXS_API int vxs_sample_batch_device(vxs_ctx* ctx, vxs_history* h, int rows, int 
                                     const double* d_u, int32_t* d_out_ids, uint32_t flags);
 
 /*
+ * Logit heads on the GPU, the step before the sampler: CodecHead and CodePredictorHead
+ * (TalkerModel.cs:133-137, Gemm.Multiply over a bf16 PackedMatrix, WeightPrecision.BFloat16):
+ *   out[r][j] = sum_k x[r][k] * W[j][k],   r < rows, j < n, k < k
+ * x fp32 [rows][ldx], W bf16 [n][ldw] (the checkpoint's [out, in] layout: talker.codec_head.weight,
+ * talker.code_predictor.lm_head.{g}.weight), out fp32 [rows][ldo], all device memory, so the
+ * logits stay on the GPU for vxs_sample_device / vxs_sample_batch_device. fp32 products and sums
+ * in an order of this library's own: each entry is within k * 2^-24 * sum_k |x w| of the exact
+ * dot product, as the reference's is. Needs k <= 2048, k and ldw multiples of 8, ldx a multiple
+ * of 4, 16-byte aligned x and W (else VXS_ERR_UNSUPPORTED). Asynchronous on the context stream.
+ */
+VXS_API int vxs_head_device(vxs_ctx* ctx, int rows, int k, int n, const float* d_x, int64_t ldx,
+                            const uint16_t* d_w, int64_t ldw, float* d_out, int64_t ldo);
+
+/*
  * Embedding rows of sampled ids, the step after the sampler, so that ids need not return to the
  * host between sampling and the next forward pass. Tables are bf16 [vocab][hidden], widened to
  * fp32 exactly (Bf16.ToFloat, src/Voxwerk/Numerics/Bf16.cs:13); sums run in the reference's order,

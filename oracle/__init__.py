@@ -6,4 +6,5 @@ package, and only as the checker or the timed CPU baseline; the product path nev
 - ``oracle.ref``: ctypes wrapper of ``libvxs_oracle.so`` (C restatement, ``vxs_oracle.c``).
 - ``oracle.sampler_np``: an independent numpy/Python restatement used to cross-check the C one.
 - ``oracle.embedding_np``: the embedding lookups of sampled ids (bf16 widening, frame sums).
+- ``oracle.head_np``: the logit heads (exact dot products and the fp32 error bound).
 """

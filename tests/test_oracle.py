@@ -425,3 +425,44 @@ def test_frame_embed_order_and_precision():
     o = np.full((2, 2), 2.0**24, np.float32)
     st = embed([0, 5], np.array([[0x3F80, 0x4000]], np.uint16), o, add=True)
     assert st.tolist() == [0, -2] and o[0].tolist() == [2.0**24, 2.0**24 + 2] and o[1, 0] == 2.0**24
+
+
+# ---------------------------------------------------------------------------------------------
+# Logit heads (oracle/head_np.py)
+# ---------------------------------------------------------------------------------------------
+def _bf16(a):
+    return (np.asarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def test_head_exact_on_integers():
+    """Small integers: every partial sum is exact in fp32, so any order gives the exact value."""
+    from oracle.head_np import head_exact
+
+    rng = np.random.default_rng(0)
+    x = rng.integers(-8, 9, (3, 1024)).astype(np.float32)
+    w = rng.integers(-8, 9, (40, 1024)).astype(np.float32)
+    want = x.astype(np.int64) @ w.astype(np.int64).T
+    assert np.array_equal(head_exact(x, _bf16(w)), want.astype(np.float64))
+
+
+def test_head_bound_holds_for_fp32_sums_in_two_orders():
+    from oracle.embedding_np import widen
+    from oracle.head_np import head_bound, head_exact
+
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((2, 1024)).astype(np.float32)
+    w = _bf16(rng.standard_normal((16, 1024)))
+    exact, bound = head_exact(x, w), head_bound(x, w)
+    wf = widen(w)
+    for r in range(2):
+        for n in range(16):
+            prods = x[r] * wf[n]  # fp32 products (rounded once each)
+            seq = np.float32(0)
+            for p in prods:  # left to right
+                seq = np.float32(seq + p)
+            pair = prods.copy()  # pairwise tree
+            while pair.size > 1:
+                pair = (pair[0::2] + pair[1::2]).astype(np.float32)
+            for got in (float(seq), float(pair[0])):
+                assert abs(got - exact[r, n]) <= bound[r, n], (r, n)
+    assert np.all(bound > 0) and np.all(bound < 1e-3 * np.abs(x).sum() * 4)

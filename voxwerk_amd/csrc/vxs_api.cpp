@@ -995,4 +995,25 @@ VXS_API int vxs_frame_embed_device(vxs_ctx* ctx, int rows, int groups, int hidde
     }
 }
 
+VXS_API int vxs_head_device(vxs_ctx* ctx, int rows, int k, int n, const float* d_x, int64_t ldx, const uint16_t* d_w,
+                            int64_t ldw, float* d_out, int64_t ldo) {
+    try {
+        if (!ctx) return VXS_ERR_INVALID_ARG;
+        if (rows < 0 || k <= 0 || n <= 0 || ldx < k || ldw < k || ldo < n)
+            return fail(ctx, VXS_ERR_INVALID_ARG, "bad rows, k, n or leading dimensions");
+        if (k > 2048 || k % 8 != 0 || ldw % 8 != 0 || ldx % 4 != 0 || ((uintptr_t)d_x & 15u) || ((uintptr_t)d_w & 15u))
+            return fail(ctx, VXS_ERR_UNSUPPORTED,
+                        "head needs k <= 2048, k and ldw multiples of 8, ldx a multiple of 4, 16-byte aligned x and w");
+        if (rows == 0) return VXS_OK;
+        if (!d_x || !d_w || !d_out) return fail(ctx, VXS_ERR_INVALID_ARG, "null pointer");
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        vxs::HeadArgs a{rows, k, n, d_x, ldx, d_w, ldw, d_out, ldo};
+        VXS_HIP(ctx, vxs::launch_head(a, ctx->stream));
+        ctx->err.clear();
+        return VXS_OK;
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
 }  // extern "C"

@@ -141,6 +141,19 @@ struct FrameEmbedArgs {
     int32_t* status;
 };
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t stream);
+
+// Logit heads (vxs_head.hip): out[r][n] = sum_k x[r][k] * W[n][k], W bf16 [n][ldw].
+// k <= 2048, k % 8 == 0, ldw % 8 == 0, ldx % 4 == 0, x and w 16-byte aligned.
+struct HeadArgs {
+    int rows, k, n;
+    const float* x;
+    int64_t ldx;
+    const uint16_t* w;
+    int64_t ldw;
+    float* out;
+    int64_t ldo;
+};
+hipError_t launch_head(const HeadArgs& a, hipStream_t stream);
 hipError_t launch_frame_embed(const FrameEmbedArgs& a, hipStream_t stream);
 
 // Enqueue the sampler on `stream`. Returns hipSuccess or the launch error.

@@ -361,7 +361,11 @@ class Context:
                                                ptr(out_ids), PATH_FLAGS[path] | RNG_FLAGS[rng])
         self._check(rc)
 
-    # embedding lookups of sampled ids (device pointers, asynchronous) ------------------------------
+    # logit heads and embedding lookups (device pointers, asynchronous) ------------------------------
+    def head_device(self, rows: int, k: int, n: int, x, ldx: int, w, ldw: int, out, ldo: int) -> None:
+        """vxs_head_device: out[r][j] = sum_k x[r][k] * W[j][k] (CodecHead / CodePredictorHead)."""
+        self._check(self._lib.vxs_head_device(self._h, rows, k, n, ptr(x), ldx, ptr(w), ldw, ptr(out), ldo))
+
     def embed_device(self, rows: int, hidden: int, ids, table, vocab: int, out, ld_out: int, add: bool, status) -> None:
         """vxs_embed_device: out[r] = table[ids[r]] or += it (CodecEmbedding / CodePredictorEmbedding)."""
         self._check(self._lib.vxs_embed_device(self._h, rows, hidden, ptr(ids), ptr(table), vocab, ptr(out), ld_out,
