@@ -50,7 +50,8 @@ def test_head_exact_on_integers(ctx, rows, k, n):
 
 @pytest.mark.parametrize("rows,k,n,pad", [(24, 1024, 3072, 0), (1, 1024, 2048, 0), (64, 1024, 3072, 8),
                                           (3, 200, 100, 0), (7, 776, 1000, 16), (9, 1536, 513, 0),
-                                          (2, 2048, 3072, 0), (4, 8, 7, 0)])
+                                          (2, 2048, 3072, 0), (4, 8, 7, 0), (2, 1024, 5, 0), (1, 1536, 3001, 8),
+                                          (1, 512, 64, 0)])
 def test_head_within_fp32_bound(ctx, rows, k, n, pad):
     rng = np.random.default_rng(rows * 1000 + k + n)
     x = rng.standard_normal((rows, k)).astype(np.float32)

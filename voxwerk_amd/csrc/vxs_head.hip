@@ -6,8 +6,8 @@
 // (1-24) this is a GEMV bound by reading W once from HBM; the products stay fp32 (no MFMA, which
 // would round x to bf16), and the logits stay in HBM for the sampler.
 //
-// Layout: a wave owns R = 8 consecutive outputs (4 when k > 1024); lane l holds W[n][k] for
-// k = 512 j + 8 l + 0..7
+// Layout: a wave owns R = 8 consecutive outputs (4 when k > 1024, 2 for one or two rows); lane l
+// holds W[n][k] for k = 512 j + 8 l + 0..7
 // (one 16-byte load per output and j, 1 KiB contiguous per wave instruction), all of its rows in
 // registers for the whole call. Per hidden row the lane loads its x slice (the next row's loads
 // issued before the current row's products), forms 8 partial dots and reduces them across the
@@ -16,6 +16,8 @@
 // output 4 b5 + 2 b4 + b3 of the wave, summed over all 64 lanes. The fp32 sum order is this kernel's own;
 // it differs from the reference's AVX-512 order by rounding only (bounded by K 2^-24 sum |x w|).
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 
 #include "vxs_internal.h"
 
@@ -43,33 +45,47 @@ __device__ __forceinline__ float dot8(u4 w, f4 xa, f4 xb, float acc) {
     return acc;
 }
 
-// One lane's slice of hidden row m: x[m][512 j + 8 lane + 0..7] for each j (zero past k).
+// One lane's slice of hidden row m: x[m][512 j + 8 lane + 0..7] for each j. FULL: k = 512 KJ, every
+// slice inside the row; otherwise slices past k read the row's start and are zeroed (a select that
+// waits for the load, so only the partial shapes pay it).
 template <int KJ>
 struct XSlice {
     f4 a[KJ], b[KJ];
 };
 
-template <int KJ>
+template <int KJ, bool FULL>
 __device__ __forceinline__ XSlice<KJ> load_x(const HeadArgs& h, int m, int lane) {
     XSlice<KJ> r;
 #pragma unroll
     for (int j = 0; j < KJ; j++) {
         const int k = 512 * j + 8 * lane;
-        const bool in = k < h.k;
+        const bool in = FULL || k < h.k;
         const float* p = h.x + (int64_t)m * h.ldx + (in ? k : 0);
         const f4 a = *reinterpret_cast<const f4*>(p);
         const f4 b = *reinterpret_cast<const f4*>(p + 4);
-        r.a[j] = in ? a : f4{0.f, 0.f, 0.f, 0.f};
-        r.b[j] = in ? b : f4{0.f, 0.f, 0.f, 0.f};
+        r.a[j] = FULL || in ? a : f4{0.f, 0.f, 0.f, 0.f};
+        r.b[j] = FULL || in ? b : f4{0.f, 0.f, 0.f, 0.f};
     }
     return r;
 }
 
-// R outputs per wave (a power of two <= 8), KJ slices of 8 per lane (k <= 512 KJ).
-template <int KJ, int R>
+// One halving exchange over lane bit `mask`: of 2H partials (outputs 2H apart in the lane pair),
+// each lane keeps the half its bit selects and adds the partner's copy of it.
+template <int H>
+__device__ __forceinline__ void halve(const float (&in)[2 * H], float (&out)[H], int lane, int mask) {
+    const bool bit = (lane & mask) != 0;
+#pragma unroll
+    for (int i = 0; i < H; i++) {
+        const float lo = in[i], hi = in[i + H];
+        out[i] = (bit ? hi : lo) + __shfl_xor(bit ? lo : hi, mask);
+    }
+}
+
+// R outputs per wave (8 or 4), KJ slices of 8 per lane (k <= 512 KJ).
+template <int KJ, int R, bool FULL>
 __global__ __launch_bounds__(kHT) void head_kernel(HeadArgs a) {
-    constexpr int kSteps = R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;  // halving exchanges
-    constexpr int kGroup = 64 >> kSteps;                                // lanes sharing an output after them
+    static_assert(R == 8 || R == 4 || R == 2, "eight, four or two outputs per wave");
+    constexpr int kGroup = 64 / R;  // lanes that share an output after the halving exchanges
     const int lane = threadIdx.x & 63;
     const int n0 = (blockIdx.x * (kHT / 64) + (threadIdx.x >> 6)) * R;
     if (n0 >= a.n) return;  // whole wave past the last output (wave-uniform)
@@ -81,24 +97,26 @@ __global__ __launch_bounds__(kHT) void head_kernel(HeadArgs a) {
 #pragma unroll
         for (int j = 0; j < KJ; j++) {
             const int k = 512 * j + 8 * lane;
-            const bool in = n0 + o < a.n && k < a.k;
+            const bool in = n0 + o < a.n && (FULL || k < a.k);
             // every lane loads from inside W (a clamped address) and zeroes what lies outside
-            const uint16_t* p = a.w + (int64_t)min(n0 + o, a.n - 1) * a.ldw + (k < a.k ? k : 0);
+            const uint16_t* p = a.w + (int64_t)min(n0 + o, a.n - 1) * a.ldw + (FULL || k < a.k ? k : 0);
             const u4 v = __builtin_nontemporal_load(reinterpret_cast<const u4*>(p));
             w[o][j] = in ? v : u4{0u, 0u, 0u, 0u};
         }
 
-    int o_mine = 0;  // output this lane holds after the halving exchanges
+    // output this lane holds after the halving exchanges (lane bits 5, 4[, 3], most significant first)
+    const int o_mine = R == 8   ? 4 * ((lane >> 5) & 1) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1)
+                       : R == 4 ? 2 * ((lane >> 5) & 1) + ((lane >> 4) & 1)
+                                : (lane >> 5) & 1;
+    // rows two at a time with two slice buffers, each reloaded in place while the other is used,
+    // so a row's loads are in flight during the previous row's products and exchanges
+    auto row = [&](int m, const XSlice<KJ>& x) {
+        if constexpr (KJ > 2) {  // keep the weights packed (widened per row): half the registers
 #pragma unroll
-    for (int s = 0; s < kSteps; s++) o_mine |= ((lane >> (5 - s)) & 1) << (kSteps - 1 - s);
-    XSlice<KJ> x = load_x<KJ>(a, 0, lane);
-    for (int m = 0; m < a.rows; m++) {
-        const XSlice<KJ> y = load_x<KJ>(a, m + 1 < a.rows ? m + 1 : m, lane);  // the next row, in flight
-        // the widening is redone per row: kept packed, the weights take half the registers
+            for (int o = 0; o < R; o++)
 #pragma unroll
-        for (int o = 0; o < R; o++)
-#pragma unroll
-            for (int j = 0; j < KJ; j++) asm volatile("" : "+v"(w[o][j]));
+                for (int j = 0; j < KJ; j++) asm volatile("" : "+v"(w[o][j]));
+        }
         float v[R];
 #pragma unroll
         for (int o = 0; o < R; o++) {
@@ -107,40 +125,71 @@ __global__ __launch_bounds__(kHT) void head_kernel(HeadArgs a) {
             for (int j = 0; j < KJ; j++) acc = dot8(w[o][j], x.a[j], x.b[j], acc);
             v[o] = acc;
         }
-        // halving exchanges over lane bits 5, 4, ...: keep the half of the outputs the bit selects
-#pragma unroll
-        for (int s = 0, half = R / 2; s < kSteps; s++, half /= 2) {
-            const int mask = 32 >> s;
-            const bool bit = (lane & mask) != 0;
-#pragma unroll
-            for (int i = 0; i < half; i++) {
-                const float send = bit ? v[i] : v[i + half];
-                const float keep = bit ? v[i + half] : v[i];
-                v[i] = keep + __shfl_xor(send, mask);
-            }
+        float sum;
+        if constexpr (R == 8) {
+            float q[4], t[2], s1[1];
+            halve<4>(v, q, lane, 32);
+            halve<2>(q, t, lane, 16);
+            halve<1>(t, s1, lane, 8);
+            sum = s1[0];
+        } else if constexpr (R == 4) {
+            float q[2], s1[1];
+            halve<2>(v, q, lane, 32);
+            halve<1>(q, s1, lane, 16);
+            sum = s1[0];
+        } else {
+            float s1[1];
+            halve<1>(v, s1, lane, 32);
+            sum = s1[0];
         }
-        float sum = v[0];
 #pragma unroll
         for (int mask = kGroup / 2; mask >= 1; mask /= 2) sum += __shfl_xor(sum, mask);
         if ((lane & (kGroup - 1)) == 0 && n0 + o_mine < a.n) a.out[(int64_t)m * a.ldo + n0 + o_mine] = sum;
-        x = y;
+    };
+    // this workgroup's rows: group blockIdx.y of a.row_group rows
+    const int first = blockIdx.y * a.row_group;
+    const int last = min(a.rows, first + a.row_group) - 1;
+    XSlice<KJ> x0 = load_x<KJ, FULL>(a, first, lane);
+    for (int m = first; m <= last; m += 2) {
+        XSlice<KJ> x1 = load_x<KJ, FULL>(a, min(m + 1, last), lane);
+        row(m, x0);
+        if (m + 1 > last) break;
+        x0 = load_x<KJ, FULL>(a, min(m + 2, last), lane);
+        row(m + 1, x1);
     }
+}
+
+// Rows are split into groups, one grid row each, so that the launch has about 2048 waves for the
+// chip's 1024 SIMDs; a group keeps at least two rows (the loads of one overlap the other's work).
+// Every group reads the weight again, from the last-level cache after the first.
+template <int KJ, int R>
+hipError_t launch_kr(HeadArgs a, hipStream_t stream) {
+    const int tiles = (a.n + (kHT / 64) * R - 1) / ((kHT / 64) * R);
+    const int waves = tiles * (kHT / 64);
+    const int groups = std::max(1, std::min(2048 / waves, a.rows / 2));
+    a.row_group = (a.rows + groups - 1) / groups;
+    const dim3 grid(tiles, (a.rows + a.row_group - 1) / a.row_group);
+    if (a.k == 512 * KJ)
+        hipLaunchKernelGGL((head_kernel<KJ, R, true>), grid, dim3(kHT), 0, stream, a);
+    else
+        hipLaunchKernelGGL((head_kernel<KJ, R, false>), grid, dim3(kHT), 0, stream, a);
+    return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_head(const HeadArgs& a, hipStream_t stream) {
     if (a.rows <= 0 || a.n <= 0) return hipSuccess;
-    const int kj = (a.k + 511) / 512;
-    auto grid = [&](int r) { return dim3((a.n + (kHT / 64) * r - 1) / ((kHT / 64) * r)); };
-    switch (kj) {  // eight outputs per wave up to k = 1024, four above (register budget)
-        case 1: hipLaunchKernelGGL((head_kernel<1, 8>), grid(8), dim3(kHT), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((head_kernel<2, 8>), grid(8), dim3(kHT), 0, stream, a); break;
-        case 3: hipLaunchKernelGGL((head_kernel<3, 4>), grid(4), dim3(kHT), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((head_kernel<4, 4>), grid(4), dim3(kHT), 0, stream, a); break;
+    // Outputs per wave: eight up to k = 1024 (four above, for registers); with one or two rows, two,
+    // so that the single pass over the weight is spread over four times as many waves.
+    const bool few = a.rows <= 2;
+    switch ((a.k + 511) / 512) {
+        case 1: return few ? launch_kr<1, 2>(a, stream) : launch_kr<1, 8>(a, stream);
+        case 2: return few ? launch_kr<2, 2>(a, stream) : launch_kr<2, 8>(a, stream);
+        case 3: return few ? launch_kr<3, 2>(a, stream) : launch_kr<3, 4>(a, stream);
+        case 4: return few ? launch_kr<4, 2>(a, stream) : launch_kr<4, 4>(a, stream);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 }  // namespace vxs

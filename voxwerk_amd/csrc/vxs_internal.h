@@ -152,6 +152,7 @@ struct HeadArgs {
     int64_t ldw;
     float* out;
     int64_t ldo;
+    int row_group;  // rows per workgroup (set by the launcher)
 };
 hipError_t launch_head(const HeadArgs& a, hipStream_t stream);
 hipError_t launch_frame_embed(const FrameEmbedArgs& a, hipStream_t stream);
