@@ -38,11 +38,11 @@ def test_wave_code_predictor(ctx):
         run_both_paths(ctx, b.logits, b.params, b.u, b.hist_off, b.hist_ids, label=f"{w.name}[{step}]")
 
 
-@pytest.mark.parametrize("vocab", [7, 64, 300, 1000, 2048, 2500, 3001, 3072])
-def test_wave_option_mixes(ctx, vocab):
+@pytest.mark.parametrize("vocab,rows", [(v, 256) for v in (7, 64, 300, 1000, 2048, 2500, 3001, 3072)] +
+                         [(3072, 2049), (1000, 2050)])  # two rows per wave from 2048 rows, odd end
+def test_wave_option_mixes(ctx, vocab, rows):
     """Mostly full-vocabulary rows (the wave path's own work), some top-k and greedy rows."""
-    rng = np.random.default_rng(2000 + vocab)
-    rows = 256
+    rng = np.random.default_rng(2000 + vocab + rows)
     scale = rng.choice([0.3, 1.0, 3.0, 8.0], size=(rows, 1))
     logits = (rng.standard_normal((rows, vocab)) * scale).astype(np.float32)
     logits[rng.random((rows, vocab)) < 0.02] += 5.0
