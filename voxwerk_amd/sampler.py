@@ -426,10 +426,14 @@ class HistoryStore:
         return out
 
     def close(self) -> None:
+        """Free the store once the context's queued work is done (freeing waits for the device)."""
         if getattr(self, "_h", None):
-            self._ctx.synchronize()
-            self._lib.vxs_history_destroy(self._h)
-            self._h = None
+            try:
+                if self._ctx.handle:
+                    self._ctx.synchronize()
+            finally:
+                self._lib.vxs_history_destroy(self._h)
+                self._h = None
 
     def __del__(self):
         try:
