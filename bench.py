@@ -163,6 +163,64 @@ def measure_head(ctx, rows: int, k: int, n: int, steps: int, hip, np) -> dict:
             "hbm_pct_peak": round(100 * gbps / HBM_PEAK_GBPS, 2)}
 
 
+def measure_device_step(ctx, rows: int, steps: int, hip, np) -> dict:
+    """The sampling side of one batched talker step with everything on the device: the talker head
+    (rows x 1024 -> 3072), the talker sampler over resident histories with device uniforms, fifteen
+    code-predictor heads (-> 2048) each followed by its sampler, and the frame embedding of the codes.
+    33 launches queued on the context stream, HIP events around the steps (no transformer layers)."""
+    from voxwerk_amd._lib import PARAMS_DTYPE
+
+    H, V, CV, G = 1024, 3072, 2048, 16
+    rng = np.random.default_rng(6)
+
+    def bf16(shape, scale):
+        return ((rng.standard_normal(shape).astype(np.float32) * scale).view(np.uint32) >> 16).astype(np.uint16)
+
+    d_x = hip.DeviceArray.from_numpy(rng.standard_normal((rows, H)).astype(np.float32))
+    d_wt, d_wc = hip.DeviceArray.from_numpy(bf16((V, H), 0.1)), hip.DeviceArray.from_numpy(bf16((G - 1, CV, H), 0.1))
+    d_et, d_ec = hip.DeviceArray.from_numpy(bf16((V, H), 1.0)), hip.DeviceArray.from_numpy(bf16((G - 1, CV, H), 1.0))
+    pt = np.zeros(rows, dtype=PARAMS_DTYPE)
+    pt["do_sample"], pt["top_k"], pt["top_p"], pt["temperature"] = 1, 50, np.float32(1.0), np.float32(0.9)
+    pt["rep_penalty"], pt["supp_begin"], pt["supp_end"], pt["keep_id"], pt["ban_id"] = np.float32(1.05), 2048, 3072, 2150, -1
+    pc = pt.copy()
+    pc["rep_penalty"], pc["supp_begin"], pc["supp_end"], pc["keep_id"] = np.float32(1.0), 0, 0, -1
+    d_pt, d_pc = hip.DeviceArray.from_numpy(pt), hip.DeviceArray.from_numpy(pc)
+    d_slots = hip.DeviceArray.from_numpy(np.arange(rows, dtype=np.int32))
+    d_lt, d_lc = hip.DeviceArray((rows, V), np.float32), hip.DeviceArray((rows, CV), np.float32)
+    d_codes = hip.DeviceArray((G, rows), np.int32)  # codebook-major: one sampling call per codebook
+    d_emb, d_st = hip.DeviceArray((rows, H), np.float32), hip.DeviceArray((rows,), np.int32)
+    warm = 10
+    store = ctx.history(rows, steps + warm + 1)
+    for s_ in range(rows):
+        store.seed(s_, 1000 + s_)
+
+    def step():
+        ctx.head_device(rows, H, V, d_x, H, d_wt, H, d_lt, V)
+        ctx.sample_batch_device(store, rows, V, d_lt, V, d_slots, d_pt, 1, None, d_codes.ptr, append=True, rng="talker")
+        for g in range(1, G):
+            ctx.head_device(rows, H, CV, d_x, H, d_wc.ptr + (g - 1) * CV * H * 2, H, d_lc, CV)
+            ctx.sample_batch_device(store, rows, CV, d_lc, CV, d_slots, d_pc, 1, None, d_codes.ptr + g * rows * 4,
+                                    append=False, rng="sub")
+        ctx.frame_embed_device(rows, G, H, d_codes, 1, d_et, V, d_ec, CV, d_emb, H, d_st, group_stride=rows)
+
+    for _ in range(warm):
+        step()
+    hip.synchronize()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(ctx.stream())
+    for _ in range(steps):
+        step()
+    e1.record(ctx.stream())
+    e1.synchronize()
+    us = e0.elapsed_ms(e1) / steps * 1e3
+    codes = d_codes.numpy()
+    assert codes.min() >= 0 and not d_st.numpy().any()
+    store.close()
+    return {"workload": f"device-resident batched step, {rows} sequences: talker head + sampler (resident "
+                        f"histories, device uniforms), 15 x (code-predictor head + sampler), frame embedding; "
+                        f"33 launches, no transformer layers", "us_per_step": round(us, 2)}
+
+
 def read_traffic():
     """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, or None."""
     try:
@@ -490,6 +548,9 @@ def main() -> int:
             m = measure_head(ctx, n_rows, 1024, n_out, 2000, hip, np)
             extra[f"{name}_{n_rows}"] = m
             log(f"[bench] {m['workload']}: {m['us_per_step']:.2f} us/step, {m['hbm_gbps']:.0f} GB/s")
+        m = measure_device_step(ctx, FRAME_ROWS, 200, hip, np)
+        extra[f"device_step_{FRAME_ROWS}"] = m
+        log(f"[bench] {m['workload']}: {m['us_per_step']:.1f} us/step")
         # embedding of the sampled frames (the step after the sampler)
         for n_rows, steps_e in ((FRAME_ROWS, 2000), (4096, 500)):
             m = measure_frame_embedding(ctx, n_rows, steps_e, hip, np)

@@ -232,10 +232,12 @@ VXS_API int vxs_embed_device(vxs_ctx* ctx, int rows, int hidden, const int32_t* 
  * (TalkerGenerator.cs:280-283, :435-439): out[r] = E0[codes[r][0]] + E1[codes[r][1]] + ... +
  * E_{groups-1}[codes[r][groups-1]] (+ addend[r] when d_addend is not NULL), left to right in fp32.
  * E0 = d_codec_table [vocab][hidden]; E_g = d_cp_tables + (g-1) * cp_vocab * hidden, g >= 1, the
- * code predictor's tables stored back to back. codes [rows][ld_codes] int32.
+ * code predictor's tables stored back to back. Code g of frame r is d_codes[r * ld_codes +
+ * g * group_stride]: a [rows][groups] matrix has ld_codes = groups, group_stride = 1; the ids of one
+ * sampling call per codebook, stage g at d_codes + g * rows, have ld_codes = 1, group_stride = rows.
  */
 VXS_API int vxs_frame_embed_device(vxs_ctx* ctx, int rows, int groups, int hidden, const int32_t* d_codes,
-                                   int64_t ld_codes, const uint16_t* d_codec_table, int vocab,
+                                   int64_t ld_codes, int64_t group_stride, const uint16_t* d_codec_table, int vocab,
                                    const uint16_t* d_cp_tables, int cp_vocab, const float* d_addend,
                                    int64_t ld_addend, float* d_out, int64_t ld_out, int32_t* d_status);
 

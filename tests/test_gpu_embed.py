@@ -65,6 +65,12 @@ def test_frame_embedding_without_text_row(ctx):
     ctx.frame_embed_device(rows, groups, hidden, d[0], groups, d[1], vocab, d[2], cp_vocab, d_out, hidden, d_st)
     ctx.synchronize()
     assert _bits_equal(d_out.numpy(), want) and not d_st.numpy().any()
+    # codebook-major codes, as one sampling call per codebook leaves them: stage g at codes + g * rows
+    d_cm, d_out2 = DeviceArray.from_numpy(np.ascontiguousarray(codes.T)), DeviceArray((rows, hidden), np.float32)
+    ctx.frame_embed_device(rows, groups, hidden, d_cm, 1, d[1], vocab, d[2], cp_vocab, d_out2, hidden, d_st,
+                           group_stride=rows)
+    ctx.synchronize()
+    assert _bits_equal(d_out2.numpy(), want) and not d_st.numpy().any()
 
 
 @pytest.mark.parametrize("add", [False, True])

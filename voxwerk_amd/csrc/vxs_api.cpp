@@ -956,13 +956,13 @@ VXS_API int vxs_embed_device(vxs_ctx* ctx, int rows, int hidden, const int32_t* 
 }
 
 VXS_API int vxs_frame_embed_device(vxs_ctx* ctx, int rows, int groups, int hidden, const int32_t* d_codes,
-                                   int64_t ld_codes, const uint16_t* d_codec_table, int vocab,
+                                   int64_t ld_codes, int64_t group_stride, const uint16_t* d_codec_table, int vocab,
                                    const uint16_t* d_cp_tables, int cp_vocab, const float* d_addend,
                                    int64_t ld_addend, float* d_out, int64_t ld_out, int32_t* d_status) {
     try {
         if (!ctx) return VXS_ERR_INVALID_ARG;
-        if (rows < 0 || groups < 1 || hidden <= 0 || vocab <= 0 || ld_codes < groups || ld_out < hidden)
-            return fail(ctx, VXS_ERR_INVALID_ARG, "bad rows, groups, hidden, vocab, ld_codes or ld_out");
+        if (rows < 0 || groups < 1 || hidden <= 0 || vocab <= 0 || ld_codes < 0 || group_stride < 0 || ld_out < hidden)
+            return fail(ctx, VXS_ERR_INVALID_ARG, "bad rows, groups, hidden, vocab, ld_codes, group_stride or ld_out");
         if (groups > 1 && (cp_vocab <= 0 || !d_cp_tables))
             return fail(ctx, VXS_ERR_INVALID_ARG, "code predictor tables missing");
         if (d_addend && ld_addend < hidden) return fail(ctx, VXS_ERR_INVALID_ARG, "ld_addend < hidden");
@@ -980,6 +980,7 @@ VXS_API int vxs_frame_embed_device(vxs_ctx* ctx, int rows, int groups, int hidde
                 (!d_addend || (ld_addend % 4 == 0 && ((uintptr_t)d_addend & 15u) == 0));
         a.codes = d_codes;
         a.ld_codes = ld_codes;
+        a.group_stride = group_stride;
         a.codec_table = d_codec_table;
         a.cp_tables = d_cp_tables;
         a.addend = d_addend;

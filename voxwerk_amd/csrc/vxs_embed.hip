@@ -87,8 +87,9 @@ __global__ __launch_bounds__(kET) void embed_kernel(EmbedArgs a) {
 __global__ __launch_bounds__(kET) void frame_embed_kernel(FrameEmbedArgs a) {
     const int r = blockIdx.x;
     const int32_t* codes = a.codes + (int64_t)r * a.ld_codes;
-    bool ok = (unsigned)codes[0] < (unsigned)a.vocab;
-    for (int g = 1; g < a.groups; g++) ok = ok && (unsigned)codes[g] < (unsigned)a.cp_vocab;
+    auto code = [&](int g) { return codes[(int64_t)g * a.group_stride]; };
+    bool ok = (unsigned)code(0) < (unsigned)a.vocab;
+    for (int g = 1; g < a.groups; g++) ok = ok && (unsigned)code(g) < (unsigned)a.cp_vocab;
     if (threadIdx.x == 0) a.status[r] = ok ? 0 : VXS_ERR_ID_OUT_OF_RANGE;
     if (!ok) return;
     float* dst = a.out + (int64_t)r * a.ld_out;
@@ -96,9 +97,9 @@ __global__ __launch_bounds__(kET) void frame_embed_kernel(FrameEmbedArgs a) {
     const bool vec = a.vec;
     for (int i = threadIdx.x * 4; i < a.hidden; i += kET * 4) {
         const int n = a.hidden - i;
-        f4 acc = gather4(a.codec_table + (int64_t)codes[0] * a.hidden + i, n, vec);
+        f4 acc = gather4(a.codec_table + (int64_t)code(0) * a.hidden + i, n, vec);
         for (int g = 1; g < a.groups; g++)
-            acc = acc + gather4(a.cp_tables + ((int64_t)(g - 1) * a.cp_vocab + codes[g]) * a.hidden + i, n, vec);
+            acc = acc + gather4(a.cp_tables + ((int64_t)(g - 1) * a.cp_vocab + code(g)) * a.hidden + i, n, vec);
         if (add) acc = acc + load4(add + i, n, vec);
         store4(dst + i, acc, n, vec);
     }
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(kET) void frame_embed16_kernel(FrameEmbedArgs a) {
     const int32_t* codes = a.codes + (int64_t)r * a.ld_codes;
     int c[kGroups];
 #pragma unroll
-    for (int g = 0; g < kGroups; g++) c[g] = codes[g];
+    for (int g = 0; g < kGroups; g++) c[g] = codes[(int64_t)g * a.group_stride];
     bool ok = (unsigned)c[0] < (unsigned)a.vocab;
 #pragma unroll
     for (int g = 1; g < kGroups; g++) ok = ok && (unsigned)c[g] < (unsigned)a.cp_vocab;

@@ -130,8 +130,8 @@ struct EmbedArgs {
 };
 struct FrameEmbedArgs {
     int rows, groups, hidden, vocab, cp_vocab, vec;
-    const int32_t* codes;  // [rows][ld_codes]
-    int64_t ld_codes;
+    const int32_t* codes;  // code g of row r at codes[r * ld_codes + g * group_stride]
+    int64_t ld_codes, group_stride;
     const uint16_t* codec_table;  // [vocab][hidden] bf16: codebook 0
     const uint16_t* cp_tables;    // [groups - 1][cp_vocab][hidden] bf16: codebooks 1..groups-1
     const float* addend;          // optional [rows][ld_addend], added last

@@ -372,9 +372,11 @@ class Context:
                                                1 if add else 0, ptr(status)))
 
     def frame_embed_device(self, rows: int, groups: int, hidden: int, codes, ld_codes: int, codec_table, vocab: int,
-                           cp_tables, cp_vocab: int, out, ld_out: int, status, addend=None, ld_addend: int = 0) -> None:
-        """vxs_frame_embed_device: FrameEmbedding of `rows` frames (+ the text row `addend`)."""
-        self._check(self._lib.vxs_frame_embed_device(self._h, rows, groups, hidden, ptr(codes), ld_codes,
+                           cp_tables, cp_vocab: int, out, ld_out: int, status, addend=None, ld_addend: int = 0,
+                           group_stride: int = 1) -> None:
+        """vxs_frame_embed_device: FrameEmbedding of `rows` frames (+ the text row `addend`); code g of
+        frame r at codes[r * ld_codes + g * group_stride]."""
+        self._check(self._lib.vxs_frame_embed_device(self._h, rows, groups, hidden, ptr(codes), ld_codes, group_stride,
                                                      ptr(codec_table), vocab, ptr(cp_tables), cp_vocab, ptr(addend),
                                                      ld_addend, ptr(out), ld_out, ptr(status)))
 
