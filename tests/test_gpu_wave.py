@@ -140,3 +140,14 @@ def test_wave_equal_mass_cuts(ctx):
             p["top_p"][r] = 0.6
     u = rng.random(rows)
     run_both_paths(ctx, x, p, u, label="equal-mass cuts")
+
+
+def test_wave_all_rows_handed_back(ctx):
+    """Every row samples with top-k, so the one-wave path flags every row for the general kernel."""
+    rng = np.random.default_rng(77)
+    rows, vocab = 2050, 3072
+    logits = (rng.standard_normal((rows, vocab)) * 2.5).astype(np.float32)
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"], p["top_k"], p["top_p"], p["temperature"] = 1, 50, np.float32(0.95), np.float32(0.9)
+    p["rep_penalty"], p["keep_id"], p["ban_id"] = np.float32(1.0), -1, -1
+    run_both_paths(ctx, logits, p, rng.random(rows), label="all handed back")

@@ -82,10 +82,8 @@ struct vxs_ctx {
     hipStream_t stream = nullptr;
     std::string err;
     DevBuf d_in, d_ids, d_logits_out, d_probs_out;
-    DevBuf d_defer;  // deferral list of the one-wave path: 2 counters, then one entry per row
+    DevBuf d_defer;  // hand-back flags of the one-wave path, one per row
     DevBuf d_draw;   // uniforms drawn on the device for a batch call (and vxs_history_draw)
-    size_t defer_rows = 0;
-    int defer_phase = 0;  // which counter the next call uses
     HostBuf h_in, h_ids, h_out;  // h_in is coherent: polled calls' kernels read it in place
     void* h_in_dev = nullptr;    // device address of h_in.p
     void* h_in_dev_of = nullptr;  // the h_in.p that h_in_dev belongs to
@@ -219,29 +217,30 @@ int choose_path(uint32_t flags, int rows, int vocab) {
     return rows >= 1024 ? vxs::kPathQuad : vxs::kPathBlock;
 }
 
-// Deferral list for `rows` rows. Both counters are zeroed when the buffer is (re)allocated; after
-// that each call's deferral kernel zeroes the counter of the call after it.
-hipError_t ensure_defer(vxs_ctx* ctx, int rows, vxs::SampleArgs& a) {
-    if ((size_t)rows > ctx->defer_rows) {
-        hipError_t e = ctx->d_defer.reserve(sizeof(int32_t) * (2 + (size_t)rows));
-        if (e != hipSuccess) return e;
-        if ((e = hipMemset(ctx->d_defer.p, 0, 2 * sizeof(int32_t))) != hipSuccess) return e;
-        ctx->defer_rows = ctx->d_defer.cap / sizeof(int32_t) - 2;
+// Host calls know their options: when most rows sample with top-k, which the one-wave path always
+// hands back, go to the one-workgroup-per-row kernel directly.
+int choose_path_host(uint32_t flags, int rows, int vocab, const vxs_params* params, int stride) {
+    const int path = choose_path(flags, rows, vocab);
+    if (path != vxs::kPathQuad || (flags & VXS_FLAG_PATH_WAVE)) return path;
+    const int np = stride == 0 ? 1 : rows;
+    int topk = 0;
+    for (int i = 0; i < np; i++) {
+        const vxs_params& p = params[(int64_t)i * stride];
+        topk += p.do_sample && p.top_k > 0 && p.top_k < vocab;
     }
-    int32_t* counts = static_cast<int32_t*>(ctx->d_defer.p);
-    a.defer_count = counts + ctx->defer_phase;
-    a.defer_next = counts + (ctx->defer_phase ^ 1);
-    a.defer_list = counts + 2;
-    ctx->defer_phase ^= 1;
+    return 2 * topk > np ? vxs::kPathBlock : path;
+}
+
+// Per-row hand-back flags of the one-wave path (written for every row by its first kernel, so no
+// clearing is needed).
+hipError_t ensure_defer(vxs_ctx* ctx, int rows, vxs::SampleArgs& a) {
+    hipError_t e = ctx->d_defer.reserve(sizeof(int32_t) * (size_t)rows);
+    if (e != hipSuccess) return e;
+    a.defer_flag = static_cast<int32_t*>(ctx->d_defer.p);
     return hipSuccess;
 }
 
-// A failed launch may leave a deferral counter unreset: zero both again before the next use.
-hipError_t launch_checked(vxs_ctx* ctx, const vxs::SampleArgs& a) {
-    const hipError_t e = vxs::launch_sample(a, ctx->stream);
-    if (e != hipSuccess) ctx->defer_rows = 0;
-    return e;
-}
+hipError_t launch_checked(vxs_ctx* ctx, const vxs::SampleArgs& a) { return vxs::launch_sample(a, ctx->stream); }
 
 int check_flags(vxs_ctx* ctx, uint32_t flags) {
     if (flags & ~kPathFlags) return fail(ctx, VXS_ERR_INVALID_ARG, "unknown flags");
@@ -393,7 +392,7 @@ int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int
     a.out_logits = want_logits ? static_cast<float*>(ctx->d_logits_out.p) : nullptr;
     a.out_probs = want_probs ? static_cast<double*>(ctx->d_probs_out.p) : nullptr;
     a.kflags = kflags;
-    a.path = choose_path(flags, rows, vocab);
+    a.path = choose_path_host(flags, rows, vocab, params, params_stride);
     if (done) {
         a.out_ids = done->out_ids;
         a.done_count = done->done_count;

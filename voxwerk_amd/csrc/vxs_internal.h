@@ -35,12 +35,9 @@ struct SampleArgs {
     double* out_probs;   // optional [rows][vocab]
     uint32_t kflags;
     int path;            // kPathBlock or kPathQuad
-    // kPathQuad: rows the one-wave path hands back, appended by it and sampled by a second
-    // kernel. Calls alternate between two counters: this call appends at *defer_count, and its
-    // second kernel zeroes *defer_next, the counter of the following call.
-    int32_t* defer_list;  // [rows]
-    int32_t* defer_count;
-    int32_t* defer_next;
+    // kPathQuad: defer_flag[r] = 1 when the one-wave path hands row r back to the general
+    // algorithm (a second kernel, one workgroup per row, samples the flagged rows), else 0.
+    int32_t* defer_flag;  // [rows]
     // Host-visible completion for small host calls (one workgroup per row): after its row, every
     // workgroup counts itself in *done_count (device memory, zero between calls); the last one
     // resets the count and stores done_seq to *done_flag (pinned host memory), which the host
