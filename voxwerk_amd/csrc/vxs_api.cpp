@@ -82,7 +82,6 @@ struct vxs_ctx {
     hipStream_t stream = nullptr;
     std::string err;
     DevBuf d_in, d_ids, d_logits_out, d_probs_out;
-    DevBuf d_defer;  // hand-back flags of the one-wave path, one per row
     DevBuf d_draw;   // uniforms drawn on the device for a batch call (and vxs_history_draw)
     HostBuf h_in, h_ids, h_out;  // h_in is coherent: polled calls' kernels read it in place
     void* h_in_dev = nullptr;    // device address of h_in.p
@@ -230,17 +229,6 @@ int choose_path_host(uint32_t flags, int rows, int vocab, const vxs_params* para
     }
     return 2 * topk > np ? vxs::kPathBlock : path;
 }
-
-// Per-row hand-back flags of the one-wave path (written for every row by its first kernel, so no
-// clearing is needed).
-hipError_t ensure_defer(vxs_ctx* ctx, int rows, vxs::SampleArgs& a) {
-    hipError_t e = ctx->d_defer.reserve(sizeof(int32_t) * (size_t)rows);
-    if (e != hipSuccess) return e;
-    a.defer_flag = static_cast<int32_t*>(ctx->d_defer.p);
-    return hipSuccess;
-}
-
-hipError_t launch_checked(vxs_ctx* ctx, const vxs::SampleArgs& a) { return vxs::launch_sample(a, ctx->stream); }
 
 int check_flags(vxs_ctx* ctx, uint32_t flags) {
     if (flags & ~kPathFlags) return fail(ctx, VXS_ERR_INVALID_ARG, "unknown flags");
@@ -401,8 +389,7 @@ int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int
     }
     if (res) set_resident(a, res->store, reinterpret_cast<const int32_t*>(d + L.hoff));
     if (res && res->rng_stream >= 0) VXS_HIP(ctx, draw_for(ctx, a, res->store, res->rng_stream));
-    if (a.path == vxs::kPathQuad) VXS_HIP(ctx, ensure_defer(ctx, rows, a));
-    VXS_HIP(ctx, launch_checked(ctx, a));
+    VXS_HIP(ctx, vxs::launch_sample(a, ctx->stream));
     if (res) {
         vxs::AppendArgs b = append_args(a, res->store, res->append);
         if (res->done) {
@@ -546,7 +533,6 @@ VXS_API void vxs_destroy(vxs_ctx* ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     ctx->d_in.release();
     ctx->d_ids.release();
-    ctx->d_defer.release();
     ctx->d_draw.release();
     ctx->d_done.release();
     ctx->h_done.release();
@@ -645,8 +631,7 @@ VXS_API int vxs_sample_device(vxs_ctx* ctx, int rows, int vocab, const float* d_
         a.out_probs = d_out_probs;
         a.kflags = 0;
         a.path = choose_path(flags, rows, vocab);
-        if (a.path == vxs::kPathQuad) VXS_HIP(ctx, ensure_defer(ctx, rows, a));
-        VXS_HIP(ctx, launch_checked(ctx, a));
+        VXS_HIP(ctx, vxs::launch_sample(a, ctx->stream));
         ctx->err.clear();
         return VXS_OK;
     } catch (...) {
@@ -916,8 +901,7 @@ VXS_API int vxs_sample_batch_device(vxs_ctx* ctx, vxs_history* h, int rows, int 
         a.kflags = 0;
         a.path = choose_path(flags, rows, vocab);
         if (rng_stream_of(flags) >= 0) VXS_HIP(ctx, draw_for(ctx, a, h, rng_stream_of(flags)));
-        if (a.path == vxs::kPathQuad) VXS_HIP(ctx, ensure_defer(ctx, rows, a));
-        VXS_HIP(ctx, launch_checked(ctx, a));
+        VXS_HIP(ctx, vxs::launch_sample(a, ctx->stream));
         VXS_HIP(ctx, vxs::launch_history_append(append_args(a, h, append != 0), ctx->stream));
         ctx->err.clear();
         return VXS_OK;

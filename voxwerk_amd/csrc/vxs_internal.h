@@ -35,9 +35,6 @@ struct SampleArgs {
     double* out_probs;   // optional [rows][vocab]
     uint32_t kflags;
     int path;            // kPathBlock or kPathQuad
-    // kPathQuad: defer_flag[r] = 1 when the one-wave path hands row r back to the general
-    // algorithm (a second kernel, one workgroup per row, samples the flagged rows), else 0.
-    int32_t* defer_flag;  // [rows]
     // Host-visible completion for small host calls (one workgroup per row): after its row, every
     // workgroup counts itself in *done_count (device memory, zero between calls); the last one
     // resets the count and stores done_seq to *done_flag (pinned host memory), which the host

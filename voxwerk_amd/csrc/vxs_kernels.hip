@@ -1325,36 +1325,39 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<
     if (a.done_flag) signal_done(a);
 }
 
-// Four rows per workgroup, one per wave, through the one-wave fast path (vxs_wave.h). A row the
-// fast path hands back is appended to the deferral list for sample_deferred_kernel.
-template <int NS>
+// Four rows per workgroup, one per wave, through the one-wave fast path (vxs_wave.h). The rows the
+// fast path hands back (every sampled row with top-k, few candidates, crowded or degenerate cuts,
+// requested outputs) are then sampled by the same workgroup with the general algorithm, one after
+// the other, in the LDS the waves no longer need: no second kernel, so nothing to launch when no
+// row is handed back, and a batch whose rows are all handed back runs one workgroup per four rows.
+template <int NS, int NC>
+union QuadSmem {
+    WaveSmem<NS> wave[kWaves];
+    RowSmem<NC> row;
+};
+
+template <int NS, int NC>
 __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void sample_quad_kernel(SampleArgs a,
                                                                                                 int vec) {
-    __shared__ WaveSmem<NS> sm[kWaves];
+    __shared__ QuadSmem<NS, NC> sm;
+    __shared__ int32_t back[kWaves];
     const int wv = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const int r = blockIdx.x * kWaves + wv;
-    if (r >= a.rows) return;
-    const int back = wave_fast_row<NS>(a, vec, r, lane, sm[wv]);
-    if (lane == 0) a.defer_flag[r] = back;
-}
-
-// The rows the one-wave path handed back, with the general algorithm: workgroup b takes rows 2b and
-// 2b + 1 when flagged and exits at once otherwise, so a batch whose rows are all handed back
-// (every sampled row with top-k) runs nearly as wide as the one-workgroup-per-row kernel, while an
-// empty hand-back dispatches half as many workgroups. Flags instead of an appended list: thousands
-// of atomic appends to one counter serialise (a fully handed-back 4096-row batch took 264 us with
-// the list and 256 workgroups, 76 us now). Four rows per workgroup in a loop spilled registers.
-template <int NC>
-__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<NC>))) void sample_deferred_kernel(
-    SampleArgs a, int vec) {
-    __shared__ RowSmem<NC> sm;
-    const int r0 = 2 * blockIdx.x, r1 = r0 + 1;
-    const int f0 = a.defer_flag[r0];
-    const int f1 = r1 < a.rows ? a.defer_flag[r1] : 0;
-    if (f0) row_block<NC>(a, vec, r0, sm);
-    if (f0 && f1) __syncthreads();  // LDS is reused by the second row
-    if (f1) row_block<NC>(a, vec, r1, sm);
+    const int r0 = blockIdx.x * kWaves;
+    const int r = r0 + wv;
+    int b = 0;
+    if (r < a.rows) b = wave_fast_row<NS>(a, vec, r, lane, sm.wave[wv]);
+    if (lane == 0) back[wv] = b;
+    __syncthreads();  // every wave is done with its LDS, and the flags are visible
+    const int b0 = back[0], b1 = back[1], b2 = back[2], b3 = back[3];  // workgroup-uniform
+    static_assert(kWaves == 4, "four rows per workgroup");
+    if (b0) row_block<NC>(a, vec, r0, sm.row);
+    if (b0 && (b1 | b2 | b3)) __syncthreads();  // LDS is reused by the next row
+    if (b1) row_block<NC>(a, vec, r0 + 1, sm.row);
+    if (b1 && (b2 | b3)) __syncthreads();
+    if (b2) row_block<NC>(a, vec, r0 + 2, sm.row);
+    if (b2 && b3) __syncthreads();
+    if (b3) row_block<NC>(a, vec, r0 + 3, sm.row);
 }
 
 template <int NC>
@@ -1365,10 +1368,8 @@ hipError_t launch_nc(const SampleArgs& a, int vec, hipStream_t stream) {
 
 template <int NS, int NC>
 hipError_t launch_quad(const SampleArgs& a, int vec, hipStream_t stream) {
-    hipLaunchKernelGGL((sample_quad_kernel<NS>), dim3((a.rows + kWaves - 1) / kWaves), dim3(kT), 0, stream, a, vec);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((sample_deferred_kernel<NC>), dim3((a.rows + 1) / 2), dim3(kT), 0, stream, a, vec);
+    hipLaunchKernelGGL((sample_quad_kernel<NS, NC>), dim3((a.rows + kWaves - 1) / kWaves), dim3(kT), 0, stream, a,
+                       vec);
     return hipGetLastError();
 }
 
