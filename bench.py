@@ -281,6 +281,21 @@ def summarize_pmc(path: str, copy_path: str, copy_mib: int) -> None:
                   f"calibrated ({len(vals)} dispatches)  {name[:90]}")
 
 
+def summarize_counters(path: str) -> None:
+    """Per-wave averages of SQ counters per kernel (a rocprofv3 --pmc counter_collection.csv):
+    each counter's per-dispatch average divided by the dispatch's SQ_WAVES (SQ_WAVES and
+    SQ_BUSY_CYCLES are shown per dispatch)."""
+    for name, counters in sorted(_read_pmc(path).items()):
+        if "copyBuffer" in name or "fillBuffer" in name:
+            continue
+        avg = {c: sum(v) / len(v) for c, v in counters.items()}
+        waves = avg.get("SQ_WAVES", 1.0) or 1.0
+        fields = " ".join(f"{c.replace('SQ_', '')}={v / (1.0 if c in ('SQ_WAVES', 'SQ_BUSY_CYCLES') else waves):.0f}"
+                          for c, v in sorted(avg.items()))
+        m = re.search(r"(\w+_kernel)(<[^>]*>)?", name)
+        print(f"{(m.group(0) if m else name[:40])} {fields}")
+
+
 def measure_device(ctx, w, steps: int, warmup: int, hip, np) -> dict:
     """Kernel time of one workload with device-resident inputs rotated over enough copies to miss
     the last-level cache; HIP events on the context stream."""
@@ -341,12 +356,17 @@ def main() -> int:
     ap.add_argument("--summarize-pmc", nargs=3, metavar=("COUNTER_CSV", "COPY_CSV", "COPY_MIB"),
                     help="per-kernel average of a rocprofv3 --pmc counter_collection.csv, calibrated by the "
                          "same counter over the copies of COPY_MIB MiB that --calibrate-copy makes")
+    ap.add_argument("--summarize-counters", metavar="CSV", help="per-wave averages of the SQ counters of a "
+                                                                  "rocprofv3 --pmc counter_collection.csv")
     ap.add_argument("--calibrate-copy", type=int, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (the counter calibration workload)")
     args = ap.parse_args()
 
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
+        return 0
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters)
         return 0
     if args.summarize_pmc:
         summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], int(args.summarize_pmc[2]))
