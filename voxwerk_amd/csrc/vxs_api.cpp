@@ -706,7 +706,12 @@ VXS_API int vxs_history_create(vxs_ctx* ctx, int slots, int cap, vxs_history** o
         h->device = ctx->device;
         h->slots = slots;
         h->cap = cap;
-        h->seeded.assign((size_t)slots, 0);
+        try {
+            h->seeded.assign((size_t)slots, 0);
+        } catch (...) {
+            delete h;
+            return fail(ctx, VXS_ERR_INVALID_ARG, "out of host memory");
+        }
         const size_t rng_bytes = sizeof(int32_t) * (size_t)slots * 2 * vxs::kRngWords;
         hipError_t e = hipMalloc(&h->ids, sizeof(int32_t) * (size_t)slots * (size_t)cap);
         if (e == hipSuccess) e = hipMalloc(&h->len, sizeof(int32_t) * (size_t)slots);
