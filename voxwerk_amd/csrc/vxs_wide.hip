@@ -1,9 +1,9 @@
 // vxs_wide.hip — the sampler for vocabularies above 8192 (up to 2^19), one 256-thread workgroup
 // per row, streaming the row from HBM instead of holding it in registers.
 //
-// Two kernels run in turn. The ordered kernel (below, sample_wide_ordered_kernel) serves the common
-// sampled top-k rows in one read of the row; the general kernel (sample_wide_kernel) serves every
-// other row and the rows the first one leaves, as follows.
+// One kernel (sample_wide_kernel), two algorithms. The ordered pass (wide_ordered_row) serves the
+// common sampled top-k rows in one read of the row; the general algorithm (wide_general_row) serves
+// every other row and the rows the ordered pass hands back, in the same workgroup, as follows.
 //
 // Pass A reads the row once (16-byte loads, 1024 entries per sweep) and applies, per entry:
 //   S1 penalty      an LDS bitmap of the history ids marks the entries to rescale (s*rho, or the
@@ -41,13 +41,11 @@ constexpr int kCapW = 512;        // candidate buffer entries per wave
 constexpr int kPerL = kCapW / 64;  // ... per lane
 constexpr int kKMax = 256;        // largest top-k of the streaming path
 constexpr int kCandW = 256;       // exact-regime capacity
-constexpr int kUnion = 1536;      // ordered kernel: the four buffers' entries after pass A, at most
+constexpr int kUnion = 1536;      // ordered pass: the four buffers' entries after pass A, at most
 constexpr int kRB = 256;          // radix buckets (8-bit digits)
 // zero words after the history bitmap: a sweep's lanes past the row end (up to 255 entries) read
 // bitmap words within the allocation
 constexpr int kBmPad = 8;
-// out_ids value the ordered kernel leaves for a row that the general kernel must serve
-constexpr int32_t kPendingId = INT32_MIN;
 
 struct WideSmem {
     uint32_t wkey[kWW][kCapW];  // per-wave candidate keys (f2key of the value)
@@ -69,10 +67,10 @@ struct WideSmem {
     };
     uint64_t slot[4][kWW];
     int32_t wcnt[kWW];  // per-wave candidate counts after pass A (-1: the wave's buffer overflowed)
-    int32_t wcomp[kWW]; // per-wave: the buffer was compacted at least once (ordered kernel)
-    int32_t wslot[kWW]; // per-wave: the wave's SIMD matches the workgroup's slot on its CU (ordered kernel)
+    int32_t wcomp[kWW]; // per-wave: the buffer was compacted at least once (ordered pass)
+    int32_t wslot[kWW]; // per-wave: the wave's SIMD matches the workgroup's slot on its CU (ordered pass)
     uint32_t tau_key;   // the largest k-th largest any wave has found so far (a shared lower bound)
-    uint32_t kth_key;   // ordered kernel: the row's k-th largest (0 without top-k) ...
+    uint32_t kth_key;   // ordered pass: the row's k-th largest (0 without top-k) ...
     float mx;           // ... and its maximum
     int32_t n;          // exact-regime candidates
 };
@@ -335,7 +333,7 @@ __device__ __forceinline__ float row_inv_temp(const vxs_params& P) {
     return !P.do_sample ? 1.0f : (P.temperature == 1.0f ? 1.0f : 1.0f / P.temperature);
 }
 
-// Rows the ordered kernel serves: sampled, 0 < k <= kKMax and k < V, 1/T finite and positive, and
+// Rows the ordered pass serves: sampled, 0 < k <= kKMax and k < V, 1/T finite and positive, and
 // no penalty or one that never raises a value (rho >= 1). For them fl(x * 1/T) bounds the
 // transformed value from above and is monotone in the raw value x.
 __device__ __forceinline__ bool row_ordered(const SampleArgs& a, const vxs_params& P) {
@@ -376,19 +374,11 @@ __device__ __forceinline__ bool build_bitmap(const BlkW& g, const SampleArgs& a,
     return true;
 }
 
-__global__ __launch_bounds__(kTW) void sample_wide_kernel(SampleArgs a, int vec) {
-    extern __shared__ uint32_t bm_dyn[];  // penalised-id bitmap, ceil(vocab / 32) words
-    __shared__ WideSmem s;
-    BlkW g;
-    g.t = threadIdx.x;
-    g.lane = g.t & 63;
-    g.wv = __builtin_amdgcn_readfirstlane(g.t >> 6);  // wave-uniform: wave ranges live in SGPRs
-    g.s = &s;
-    const int r = blockIdx.x;
+// The general algorithm for row r (every option mix; the rows the ordered pass leaves).
+__device__ __forceinline__ void wide_general_row(const SampleArgs& a, int vec, int r, BlkW& g, WideSmem& s,
+                                                 uint32_t* bm_dyn) {
     const int V = a.vocab;
     const vxs_params P = a.params[(int64_t)r * a.params_stride];
-    const int prior = a.out_ids[r];  // read alongside the options
-    if (row_ordered(a, P) && prior != kPendingId) return;  // served by the ordered kernel
     const float* __restrict__ xrow = a.logits + (int64_t)r * a.ld;
     float* orow = a.out_logits ? a.out_logits + (int64_t)r * V : nullptr;
     double* prow = a.out_probs ? a.out_probs + (int64_t)r * V : nullptr;
@@ -955,7 +945,8 @@ __device__ __forceinline__ float x_threshold(float tau, float invT) {
 }
 
 // =====================================================================================
-// The ordered kernel: the rows row_ordered() selects, in one read of the row.
+// The ordered pass: the rows row_ordered() selects, in one read of the row. Returns true when the
+// general algorithm must serve the row instead.
 //
 // Pass A: each wave streams its quarter of the row and keeps a buffer of raw values and indices.
 // The exact transformed value v (penalty, suppression, temperature) is at most fl(x * 1/T), which
@@ -972,21 +963,13 @@ __device__ __forceinline__ float x_threshold(float tau, float invT) {
 // reference's sequential fp64 arithmetic (S6-S8, Sampler.cs:51-87). The (d, index) order is the
 // reference's (p, index) order whenever each adjacent pair is in (p, index) order (p = exp(d) / sum
 // never decreases with d for a monotone exp); otherwise the candidates are ranked by p directly.
-// Rows that end with too many tied candidates are marked kPendingId for the general kernel.
+// Rows that end with too many tied candidates go to the general algorithm.
 // =====================================================================================
-__global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void sample_wide_ordered_kernel(
-    SampleArgs a, int vec) {
-    extern __shared__ uint32_t bm_dyn[];
-    __shared__ WideSmem s;
-    BlkW g;
-    g.t = threadIdx.x;
-    g.lane = g.t & 63;
-    g.wv = __builtin_amdgcn_readfirstlane(g.t >> 6);
-    g.s = &s;
-    const int r = blockIdx.x;
+__device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, int r, BlkW& g, WideSmem& s,
+                                                 uint32_t* bm_dyn) {
     const int V = a.vocab;
     const vxs_params P = a.params[(int64_t)r * a.params_stride];
-    if (!row_ordered(a, P)) return;  // the general kernel serves it
+    if (!row_ordered(a, P)) return true;  // the general algorithm serves it
     const float* __restrict__ xrow = a.logits + (int64_t)r * a.ld;
     const float invT = row_inv_temp(P);
     const int K = P.top_k;
@@ -1019,7 +1002,7 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
     X.rinv = 1.0f / P.rep_penalty;
     X.fastdiv = __builtin_fabsf(P.rep_penalty) >= 0x1p-60f && __builtin_fabsf(P.rep_penalty) <= 0x1p60f;
     if (P.rep_penalty != 1.0f && has_history(a)) {
-        if (!build_bitmap(g, a, r, V, bm_dyn)) return;
+        if (!build_bitmap(g, a, r, V, bm_dyn)) return false;
         X.bm = bm_dyn;
     }
     X.sb = max(P.supp_begin, 0);
@@ -1034,7 +1017,7 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
     // ---- pass A
     uint32_t* wkey = s.wkey[g.wv];
     int32_t* widx = s.widx[g.wv];
-    // kStop: the wave stopped collecting (the general kernel then serves the row); kCompacted: its
+    // kStop: the wave stopped collecting (the general algorithm then serves the row); kCompacted: its
     // buffer was compacted at least once. One word, only ever or-ed: two flag variables had their
     // stores merged behind a selected address, which kept them in scratch memory.
     constexpr uint32_t kStop = 1u, kCompacted = 2u;
@@ -1126,7 +1109,7 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
                     cnt = 0;
 #pragma unroll
                     for (int j = 0; j < 4; j++) cnt += __builtin_popcountll(__ballot(xv[j] >= xt));
-                    if (wn + cnt > kCapW) state |= kStop;  // ties: the general kernel
+                    if (wn + cnt > kCapW) state |= kStop;  // ties: the general algorithm
                 }
                 if (cnt == 0 || (state & kStop)) continue;
                 const int i0 = base + 4 * g.lane;
@@ -1196,7 +1179,7 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
         for_row(xrow, V, vec, g.t, X, [&](int, float v) { bad |= __builtin_amdgcn_class(v, 0x203); });
     if (g.any(bad)) {
         if (g.t == 0) a.out_ids[r] = VXS_ERR_NONFINITE;
-        return;
+        return false;
     }
     // The finite count is the buffered total unless some wave compacted, which takes more than k
     // finite entries (a count of "many" decides top-k the same way).
@@ -1209,8 +1192,7 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
         tot += (uint32_t)max(s.wcnt[w], 0);
     }
     if (!all || tot > (uint32_t)kUnion) {  // a wave stopped collecting, or ties fill the buffers
-        if (g.t == 0) a.out_ids[r] = kPendingId;
-        return;
+        return true;  // the general algorithm takes the row
     }
     const uint32_t cnt = comp ? (uint32_t)V : tot;
     float* orow = a.out_logits ? a.out_logits + (int64_t)r * V : nullptr;
@@ -1220,7 +1202,7 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
         if (orow) for_row(xrow, V, vec, g.t, X, [&](int i, float x) { orow[i] = x; });
         if (prow)
             for (int i = g.t; i < V; i += kTW) prow[i] = __builtin_nan("");
-        return;
+        return false;
     }
     const bool topk_on = (uint32_t)K < cnt;
     uint64_t* ckey = reinterpret_cast<uint64_t*>(s.ex.cp);  // (d, index) keys before the probabilities
@@ -1283,8 +1265,7 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
     const float kth = topk_on ? key2f(s.kth_key) : kNegInf;
     const float mx = s.mx;
     if (n > kCandW) {  // ties beyond the exact-regime capacity
-        if (g.t == 0) a.out_ids[r] = kPendingId;
-        return;
+        return true;  // the general algorithm takes the row
     }
     if (orow) for_row(xrow, V, vec, g.t, X, [&](int i, float x) { orow[i] = x < kth ? kNegInf : x; });
     if (prow)
@@ -1312,7 +1293,7 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
         s.ex.cs[po] = (int16_t)io;
     }
     __syncthreads();
-    if (!worker) return;
+    if (!worker) return false;
 
     // ---- the worker wave: the reference's fp64 arithmetic on the candidates in index order
     double* cp = s.ex.cp;
@@ -1360,6 +1341,24 @@ __global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void s
     if (g.lane == 0) a.out_ids[r] = pick;
     if (prow)
         for (int j = g.lane; j < n; j += 64) prow[s.ex.ci[j]] = cp[j];
+    return false;
+}
+
+// One workgroup per row: the ordered pass when the row's options allow it, else (or when that pass
+// hands the row back) the general algorithm, in the same workgroup.
+__global__ __launch_bounds__(kTW) __attribute__((amdgpu_waves_per_eu(4))) void sample_wide_kernel(SampleArgs a,
+                                                                                                 int vec) {
+    extern __shared__ uint32_t bm_dyn[];  // penalised-id bitmap, ceil(vocab / 32) words
+    __shared__ WideSmem s;
+    BlkW g;
+    g.t = threadIdx.x;
+    g.lane = g.t & 63;
+    g.wv = __builtin_amdgcn_readfirstlane(g.t >> 6);  // wave-uniform: wave ranges live in SGPRs
+    g.s = &s;
+    const int r = blockIdx.x;
+    if (!wide_ordered_row(a, vec, r, g, s, bm_dyn)) return;
+    __syncthreads();  // the ordered pass is done with the LDS
+    wide_general_row(a, vec, r, g, s, bm_dyn);
 }
 
 }  // namespace
@@ -1369,8 +1368,6 @@ hipError_t launch_sample_wide(const SampleArgs& a, hipStream_t stream) {
     if (a.vocab <= 0 || a.vocab > kWideMaxVocab) return hipErrorNotSupported;
     const int vec = (a.ld % 4 == 0) && (((uintptr_t)a.logits & 15u) == 0) ? 1 : 0;
     const size_t dyn = sizeof(uint32_t) * (size_t)((a.vocab + 31) / 32 + kBmPad);
-    // the ordered kernel first; the general kernel serves every other row and the rows it left
-    hipLaunchKernelGGL(sample_wide_ordered_kernel, dim3(a.rows), dim3(kTW), dyn, stream, a, vec);
     hipLaunchKernelGGL(sample_wide_kernel, dim3(a.rows), dim3(kTW), dyn, stream, a, vec);
     return hipGetLastError();
 }
