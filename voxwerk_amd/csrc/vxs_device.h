@@ -457,12 +457,13 @@ __device__ __forceinline__ int seq_rank(const double* p, int n, int j) {
     return rank;
 }
 
-// Nucleus mass of a weight q in [0, 1]: fl32(fl32(q + Cb) - Cb) with Cb = 2^(23 - F), a multiple of
-// 2^-F within 1.5 ulp of q (fl32(q + Cb) >= Cb has an ulp of at least 2^-F; below Cb the subtraction
-// is exact, and every fp32 value at or above Cb is a multiple of 2^-F). Sums of up to 2^(53-F) such
-// masses are exact in double precision, so partial sums and LDS atomics are order-independent.
+// Nucleus mass of a weight q in [0, 1], a multiple of 2^-F: q itself when q >= Cb = 2^(23 - F) (every
+// fp32 value there is a multiple of 2^-F), else fl32(fl32(q + Cb) - Cb), q rounded to the nearest
+// multiple of 2^-F (fl32(q + Cb) lies in [Cb, 2 Cb], where the ulp is 2^-F, and the subtraction is
+// exact). Monotone in q. Sums of up to 2^(53-F) such masses are exact in double precision, so
+// partial sums and LDS atomics are order-independent.
 __device__ __forceinline__ float mass_bias(int F) { return __uint_as_float((uint32_t)(150 - F) << 23); }
-__device__ __forceinline__ float mass_of(float q, float Cb) { return (q + Cb) - Cb; }
+__device__ __forceinline__ float mass_of(float q, float Cb) { return q >= Cb ? q : (q + Cb) - Cb; }
 // The same mass as an integer-valued double (units of 2^-F).
 __device__ __forceinline__ double fixed_mass(float q, float Cb, double scaleF) { return (double)mass_of(q, Cb) * scaleF; }
 
@@ -487,6 +488,19 @@ __device__ __forceinline__ float penalize_fast(float s, float rho, float rinv) {
 }
 __device__ __forceinline__ bool penalize_needs_division(float s, bool fast) {
     return !(s < 0.0f) && !(fast && s >= 0x1p-60f && s <= 0x1p60f);
+}
+
+// Nucleus weight of d = x - max <= 0 for vocabularies up to 8192 (the one-wave and one-workgroup
+// kernels): 2^fl32(d * fl32(log2 e)) with the hardware 2^x, three VALU operations. Monotone
+// non-decreasing in d (one rounding of a product by a positive constant, then a monotone 2^x; both
+// checked on every float of [-128, 0] by vxs_selfcheck). Relative error at most |d| * 7.4e-8 plus
+// the 2^x rounding: the rounding of d * log2e to fp32 (half an ulp of |d| * 1.44) and the 1.3e-8
+// relative error of the constant, each scaled by ln 2. Over a row the mass-weighted error of any
+// cumulative sum is at most E_p[|d|] * 7.4e-8 + 1.2e-7 relative to the total, below 6e-7 for every
+// row of at most 8192 entries (E_p[|d|] <= 6.3 there), inside the 1e-6 band in which a draw or a
+// top-p cut may differ from the reference's. -inf gives 0.
+__device__ __forceinline__ float nucleus_exp(float d) {
+    return __builtin_amdgcn_exp2f(d * 1.44269502162933349609375f);
 }
 
 // exp(d) for d <= 0 in fp32: 2^(d log2 e) with the product carried in two parts (the rounding

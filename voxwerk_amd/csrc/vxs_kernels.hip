@@ -1007,7 +1007,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
     auto qof = [&](int e) -> double {
         float x = v[e];
         asm volatile("" : "+v"(x));
-        return fixed_mass(exp_neg(x), Cb, scaleF);
+        return fixed_mass(nucleus_exp(x), Cb, scaleF);
     };
     auto keyof = [&](int e) -> uint32_t {
         float x = v[e];
@@ -1032,7 +1032,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
         };
 #pragma unroll
         for (int e = 0; e < NE; e++)  // -inf entries add 0 to bucket 0
-            atomicAdd(&sm.u.nh[e >> 2][bk(e)], fixed_mass(exp_neg(v[e]), Cb, scaleF));
+            atomicAdd(&sm.u.nh[e >> 2][bk(e)], fixed_mass(nucleus_exp(v[e]), Cb, scaleF));
         if (g.t == 0) {
             sm.ctl.bstar = -1;
             sm.ctl.list_n = 0;
@@ -1226,7 +1226,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
         for (int c = 0; c < NC; c++) {
             double s2 = 0.0;
 #pragma unroll
-            for (int j = 0; j < 4; j++) s2 += fixed_mass(exp_neg(v[c * 4 + j]), Cb, scaleF);
+            for (int j = 0; j < 4; j++) s2 += fixed_mass(nucleus_exp(v[c * 4 + j]), Cb, scaleF);
             const double w = wave_sum(s2);
             if (g.lane == 0) g.slot[kSiteChunk0 + c][g.wv] = (uint64_t)__double_as_longlong(w);
         }

@@ -169,11 +169,18 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
     // the penalised value back: a wave's LDS operations execute in order, so all reads precede all
     // writes and a repeated id writes the same value again instead of being penalised twice. The
     // reads and writes are unmasked: an id outside the part uses the lane's own spare slot.
+    // The quotient is the Markstein-corrected one (penalize_fast): correctly rounded for rho with
+    // |rho| in [2^-20, 2^20] (other rows go to the general path) and logits in [2^-60, 2^60] or
+    // negative. The rest cannot change the sampled id here: -0 becomes +0, which gives the same d
+    // and mass and compares equal; a positive logit below 2^-60, off by at most 2^-83, gives the
+    // same d = fl32(x - max) when the maximum is at least 2^-30, and a row whose maximum lies in
+    // (0, 2^-30) or at or above 2^100 (or is not finite) goes to the general path after the
+    // statistics below.
     if (pen_on && h1 > h0) {
         const float rho = P.rep_penalty;
-        const float rinv = 1.0f / rho;
         const float arho = __builtin_fabsf(rho);
-        const bool fast = arho >= 0x1p-60f && arho <= 0x1p60f;
+        if (!(arho >= 0x1p-20f && arho <= 0x1p20f)) return 1;
+        const float rinv = 1.0f / rho;
         bool live[kHP];
         bool bad = false;
 #pragma unroll
@@ -199,21 +206,11 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
             {
                 int at[kHP];
                 float pv[kHP];
-                bool slow = false;
 #pragma unroll
                 for (int k = 0; k < kHP; k++) {
                     const bool in = live[k] && (unsigned)(pre[k] - lo) < (unsigned)span;
                     at[k] = in ? pre[k] - lo : kPart * kSweep + lane;
-                    const float sv = xs[at[k]];
-                    pv[k] = penalize_fast(sv, rho, rinv);
-                    slow |= in && penalize_needs_division(sv, fast);
-                }
-                if (__ballot(slow)) {  // zeros, non-finite or extreme values: IEEE division
-#pragma unroll
-                    for (int k = 0; k < kHP; k++) {
-                        const float sv = xs[at[k]];
-                        if (penalize_needs_division(sv, fast)) pv[k] = sv / rho;
-                    }
+                    pv[k] = penalize_fast(xs[at[k]], rho, rinv);
                 }
 #pragma unroll
                 for (int k = 0; k < kHP; k++) xs[at[k]] = pv[k];
@@ -256,6 +253,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         }
         wave_argmax(bv, bi);
         const bool anynan = __ballot(nan) != 0;
+        if (pen_on && (anynan || bv >= 0x1p100f || (bv > 0.0f && bv < 0x1p-30f))) return 1;  // see S1
         if (lane == 0) a.out_ids[r] = anynan ? VXS_ERR_NONFINITE : bi;
         return 0;
     }
@@ -283,10 +281,12 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
             tmn = fminf(tmn, v[e]);
         }
         if (__ballot(!(tmx < kPosInf))) {
+            if (pen_on) return 1;  // a penalised non-finite logit: the general path reports it
             if (lane == 0) a.out_ids[r] = VXS_ERR_NONFINITE;
             return 0;
         }
         mx = wave_fmax(tmx);
+        if (pen_on && (mx >= 0x1p100f || (mx > 0.0f && mx < 0x1p-30f))) return 1;  // see S1
         mn = wave_fmin(tmn);
         fmn = mn;
         cnt = (uint32_t)V;
@@ -320,14 +320,21 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
     // 2^F and 2^-F built from their bits, so they stay in scalar registers
     const double gF = __longlong_as_double((long long)(1023 + F) << 52);
     const double gFi = __longlong_as_double((long long)(1023 - F) << 52);
-    // masses replace the logits: exp(x - max) in fp32 on the 2^-F grid; -inf entries get 0
-    if (mn != kNegInf && fmn - mx >= -256.0f) {  // every d in [-256, 0]: exp_neg's clamp is the identity
+    // d = x - max replaces the logits (-inf stays -inf); the low byte of each d's bits is kept, one
+    // byte per entry (dl[c] byte j is entry 4c + j of the lane), to order entries of equal mass by d
+    uint32_t dl[NS];
 #pragma unroll
-        for (int e = 0; e < NE; e++) v[e] = mass_of(exp_neg_unclamped(v[e] - mx), Cb);
-    } else {
+    for (int e = 0; e < NE; e++) v[e] = v[e] - mx;
 #pragma unroll
-        for (int e = 0; e < NE; e++) v[e] = mass_of(exp_neg(v[e] - mx), Cb);
+    for (int c = 0; c < NS; c++) {
+        const uint32_t lo01 = __builtin_amdgcn_perm(__float_as_uint(v[4 * c + 1]), __float_as_uint(v[4 * c]), 0x0c0c0400u);
+        const uint32_t lo23 = __builtin_amdgcn_perm(__float_as_uint(v[4 * c + 3]), __float_as_uint(v[4 * c + 2]), 0x0c0c0400u);
+        dl[c] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
     }
+    // masses replace d: nucleus_exp(d), on the 2^-F grid. When the smallest is at least 2^(23-F)
+    // (and no entry is -inf) every mass is a multiple of 2^-F already and the rounding is skipped.
+    const float qmin = mass_of(nucleus_exp(fmn - mx), Cb);
+    const bool ongrid = mn != kNegInf && qmin >= Cb;
     float qc = 0.0f;  // cut: keep masses >= qc
     double Skept;
     if (topp) {
@@ -335,7 +342,6 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         // Buckets: bits(mass) >> sh, a log scale, 1024 of them from `base` up. Every nonzero mass
         // lies in [lb, bits(1) + 8]; zero masses land anywhere and add nothing. The physical
         // bucket is the low 10 bits of the index, so no clamp is needed.
-        const float qmin = mass_of(exp_neg(fmn - mx), Cb);
         const float qlow = qmin - qmin * 0x1p-18f - __uint_as_float((uint32_t)(127 - F) << 23);
         const uint32_t lb = max(__float_as_uint(qlow), (uint32_t)(127 - F) << 23);
         constexpr uint32_t kTop = 0x3f800000u + 8u;
@@ -343,28 +349,74 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         if ((kTop >> sh) + 2 - ((lb >> sh) & ~15u) > (uint32_t)kNB - 1) sh++;
         const uint32_t base = (lb >> sh) & ~15u;
         const uint32_t pbase = (base + (uint32_t)(kBPL * lane)) & (kNB - 1);
+        // Packed buckets when every mass is on the grid and a bucket lies inside one binade
+        // (sh <= 19: a lane's 16 buckets then share their exponent): each entry adds its count
+        // (high word) and its mantissa bits below the bucket's (low word, below 2^31 for 3072
+        // entries), from which the bucket's mass follows exactly. Otherwise each entry adds its
+        // mass in units of 2^-F.
+        const bool packed = ongrid && sh <= 19;
 #pragma unroll
         for (int i = 0; i < kNB / 128; i++) *(dbl2*)&s.hist[(i * 64 + lane) * 2] = dbl2{0.0, 0.0};  // zero bits
         wsync();
-        // Integer atomics (LDS adds u64 faster than f64): a mass below 2^(52-F) added to 2^(52-F) in
-        // double precision leaves mass * 2^F, an integer below 2^52, in the mantissa bits (the sum
-        // keeps the exponent of 2^(52-F), so the high word just loses its exponent bits).
-        const double big = __longlong_as_double((long long)(1023 + 52 - F) << 52);
+        // the masses and their histogram atomics in one pass, so the atomics drain while the
+        // remaining masses are computed
+        if (packed) {
+            const uint32_t lmask = (1u << sh) - 1u;
 #pragma unroll
-        for (int e = 0; e < NE; e++) {
-            const uint64_t tb = (uint64_t)__double_as_longlong((double)v[e] + big);
-            const uint64_t iq = (tb & 0xffffffffull) | ((uint64_t)((uint32_t)(tb >> 32) & 0xfffffu) << 32);
-            atomicAdd((unsigned long long*)&s.hist[__builtin_amdgcn_ubfe(__float_as_uint(v[e]), (uint32_t)sh, 10u)],
-                      (unsigned long long)iq);
+            for (int e = 0; e < NE; e++) {
+                const float q = nucleus_exp(v[e]);
+                v[e] = q;
+                const uint32_t qb = __float_as_uint(q);
+                atomicAdd((unsigned long long*)&s.hist[__builtin_amdgcn_ubfe(qb, (uint32_t)sh, 10u)],
+                          (unsigned long long)(qb & lmask) | (1ull << 32));
+            }
+        } else {
+            // Integer atomics (LDS adds u64 faster than f64): a mass below 2^(52-F) added to
+            // 2^(52-F) in double precision leaves mass * 2^F, an integer below 2^52, in the
+            // mantissa bits (the sum keeps the exponent of 2^(52-F), so the high word just loses
+            // its exponent bits).
+            const double big = __longlong_as_double((long long)(1023 + 52 - F) << 52);
+#pragma unroll
+            for (int e = 0; e < NE; e++) {
+                const float q = ongrid ? nucleus_exp(v[e]) : mass_of(nucleus_exp(v[e]), Cb);
+                v[e] = q;
+                const uint64_t tb = (uint64_t)__double_as_longlong((double)q + big);
+                const uint64_t iq = (tb & 0xffffffffull) | ((uint64_t)((uint32_t)(tb >> 32) & 0xfffffu) << 32);
+                atomicAdd((unsigned long long*)&s.hist[__builtin_amdgcn_ubfe(__float_as_uint(q), (uint32_t)sh, 10u)],
+                          (unsigned long long)iq);
+            }
         }
         wsync();
+        // mass of logical bucket (base + 16 * bl + j) in units of 2^-F from its packed entry
+        auto packed_units = [&](uint32_t bl, uint32_t j, uint64_t ent) -> uint64_t {
+            const uint32_t t = (base + 16u * bl + j) << sh;  // bits of the bucket's smallest value
+            const int sft = (int)(t >> 23) + F - 150;
+            const uint64_t m = (uint64_t)((t & 0x7fffffu) | 0x800000u) * (uint32_t)(ent >> 32) + (uint32_t)ent;
+            return sft >= 0 ? m << sft : 0ull;  // empty below the range
+        };
         // lane totals in ascending bucket order, then the crossing lane, then the crossing bucket;
         // lane l reads its 16 buckets in the order j xor (l/2 mod 16), which spreads every read of
         // the wave over all LDS banks
         uint64_t lti = 0;
         const int rot = (lane >> 1) & (kBPL - 1);
+        if (packed) {
+            uint32_t N = 0, J = 0, Lo = 0;
 #pragma unroll
-        for (int j = 0; j < kBPL; j++) lti += s.hist[pbase + (j ^ rot)];
+            for (int j = 0; j < kBPL; j++) {
+                const uint64_t ent = s.hist[pbase + (j ^ rot)];
+                N += (uint32_t)(ent >> 32);
+                J += (uint32_t)(j ^ rot) * (uint32_t)(ent >> 32);
+                Lo += (uint32_t)ent;
+            }
+            // the 16 buckets share their exponent: sum of n_j * (M_0 + j * 2^sh) + low_j
+            const uint32_t t0 = (base + 16u * (uint32_t)lane) << sh;
+            const int sft = (int)(t0 >> 23) + F - 150;
+            const uint64_t m = (uint64_t)((t0 & 0x7fffffu) | 0x800000u) * N + Lo + ((uint64_t)J << sh);
+            lti = sft >= 0 ? m << sft : 0ull;
+        } else {
+#pragma unroll
+            for (int j = 0; j < kBPL; j++) lti += s.hist[pbase + (j ^ rot)];
+        }
         const double lt = (double)lti * gFi;  // exact: below 2^53 units of 2^-F
         const double incl = wave_incl_sum(lt);
         const double S = readlane_d(incl, 63);
@@ -375,7 +427,9 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         const int L = (int)__builtin_ctzll(cb);
         const double runL = readlane_d(run, L);
         const uint32_t pL = (base + (uint32_t)(kBPL * L)) & (kNB - 1);
-        const double hj = lane < kBPL ? (double)s.hist[pL + (lane & (kBPL - 1))] * gFi : 0.0;
+        const uint64_t hent = s.hist[pL + (lane & (kBPL - 1))];
+        const uint64_t hu = packed ? packed_units((uint32_t)L, (uint32_t)(lane & (kBPL - 1)), hent) : hent;
+        const double hj = lane < kBPL ? (double)hu * gFi : 0.0;
         const double ij = row_incl_sum(hj);  // lanes 0..15 form one DPP row
         const double xj = runL + (ij - hj);
         const uint64_t jb = __ballot(lane < kBPL && xj <= T && T - xj < hj);
@@ -384,19 +438,31 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         const double below = readlane_d(xj, jl);
         const uint32_t glo = (base + (uint32_t)(kBPL * L + jl)) << sh;  // bits of the bucket's masses
         const uint32_t gw = 1u << sh;
-        // gather the crossing bucket (ballot compaction)
+        // gather the crossing bucket (ballot compaction); the compares of a batch of eight slots
+        // are issued before their ballots are consumed
         uint32_t n = 0;
         uint32_t gwo = gw;
         asm volatile("" : "+s"(gwo));  // a plain unsigned compare (not rewritten into a shift and a test)
+        uint32_t* kw = reinterpret_cast<uint32_t*>(s.key);
 #pragma unroll
-        for (int e = 0; e < NE; e++) {
-            const uint32_t qb = __float_as_uint(v[e]);
-            const bool p = qb - glo < gwo;
-            const uint64_t bal = __ballot(p);
-            if (bal) {
-                const uint32_t pos = n + mbcnt(bal);
-                if (p && pos < (uint32_t)kL) s.key[pos] = ((uint64_t)qb << 32) | (uint32_t)eidx(e);
-                n += (uint32_t)__builtin_popcountll(bal);
+        for (int e0 = 0; e0 < NE; e0 += 8) {
+            bool p[8];
+            uint64_t bal[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                p[k] = __float_as_uint(v[e0 + k]) - glo < gwo;
+                bal[k] = __ballot(p[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                if (bal[k]) {
+                    const uint32_t pos = n + mbcnt(bal[k]);
+                    if (p[k] && pos < (uint32_t)kL) {  // key: mass bits << 32 | index, as two words
+                        kw[2 * pos] = (uint32_t)eidx(e0 + k);
+                        kw[2 * pos + 1] = __float_as_uint(v[e0 + k]);
+                    }
+                    n += (uint32_t)__builtin_popcountll(bal[k]);
+                }
             }
         }
         if (n > (uint32_t)kL) return 1;
@@ -423,55 +489,102 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         const int rl = (int)__builtin_ctzll(rb);
         const uint32_t kc = (uint32_t)(s.skey[rl] >> 32);
         qc = __uint_as_float(kc);
-        // The masses are a monotone function of the logit (exp_neg is monotone on gfx950 —
-        // checked over every float in [-128, 0] — and the rounding to the 2^-F grid is
-        // monotone), so (mass, index) order is (logit, index) order except inside a group of
-        // equal masses. A cut inside such a group keeps its higher indices, which is the
-        // reference's choice when the group's logits are equal; they are wherever the cut's mass
-        // lies in [2^-16, 2^-6] (logits 4 to 11 below the max, where distinct logits never share a
-        // mass). A cut inside a group elsewhere sends the row to the general path.
+        // The masses are a monotone function of d (nucleus_exp is monotone on gfx950 — checked
+        // over every float in [-128, 0] — and so is the rounding to the 2^-F grid), so (mass,
+        // index) order is the reference's (d, index) order except inside a group of equal masses,
+        // whose d may still differ: one rounding of d * log2 e can merge neighbouring values of d.
+        // A cut inside such a group removes the group's first rl - g0 members in (d, index) order.
+        // Where the mass is at most 1/2, equal masses imply d within a few ulps of each other, so
+        // the low bytes of their bits order them (modulo 256; larger bits, smaller d). Above 1/2
+        // (d within 0.7 of the max) a group can span many ulps: the general path takes the row.
         if (rl > 0 && (uint32_t)(s.skey[rl - 1] >> 32) == kc) {
-            if (!(qc >= 0x1p-16f && qc <= 0x1p-6f)) return 1;
-            // the group's entries below the cut index are removed: their masses become 0
-            const int ic = (int)(uint32_t)s.skey[rl];
+            if (!(qc <= 0.5f)) return 1;
+            int g0 = rl - 1;
+            while (g0 > 0 && (uint32_t)(s.skey[g0 - 1] >> 32) == kc) g0--;
+            int g1 = rl + 1;
+            while (g1 < nn && (uint32_t)(s.skey[g1] >> 32) == kc) g1++;
+            // every member's low byte of d, fetched from the lane and register that hold it
+            const bool mem = lane >= g0 && lane < g1;
+            const uint32_t mi = mem ? (uint32_t)s.skey[lane] : 0u;
+            const int ol = (int)((mi >> 2) & 63u);
+            uint32_t word = 0;
+#pragma unroll
+            for (int c = 0; c < NS; c++) {
+                const uint32_t t = (uint32_t)__builtin_amdgcn_ds_bpermute(ol * 4, (int)dl[c]);
+                word = (int)(mi >> 8) == c ? t : word;
+            }
+            const uint32_t dlow = (word >> (8 * (mi & 3u))) & 0xffu;
+            const uint32_t ref = readlane(dlow, g0);
+            const int rel = (int)(int8_t)(uint8_t)(dlow - ref);  // larger: larger bits, smaller d
+            if (__ballot(mem && (rel > 32 || rel < -32))) return 1;
+            // order key: smaller d first, then smaller index
+            uint32_t* ok = reinterpret_cast<uint32_t*>(s.ws);
+            if (mem) ok[lane] = ((uint32_t)(127 - rel) << 16) | mi;
+            wsync();
+            uint32_t grk = 0;
+            const uint32_t mine = mem ? ok[lane] : 0u;
+            for (int b = g0; b < g1; b++) grk += ok[b] < mine ? 1u : 0u;
+            const bool removed = mem && (int)grk < rl - g0;
+            // removed members' masses become 0: each sets its bit in its owner lane's mask
+            wsync();
+            uint64_t* msk = reinterpret_cast<uint64_t*>(s.ws);
+            msk[lane] = 0;
+            wsync();
+            if (removed) atomicOr((unsigned long long*)&msk[ol], 1ull << ((mi >> 8) * 4 + (mi & 3u)));
+            wsync();
+            const uint64_t mm = msk[lane];
 #pragma unroll
             for (int e = 0; e < NE; e++)
-                if (v[e] == qc && eidx(e) < ic) v[e] = 0.0f;
+                if ((mm >> e) & 1ull) v[e] = 0.0f;
         }
         Skept = S - readlane_d(c0, rl);
     } else {
+        if (ongrid) {
+#pragma unroll
+            for (int e = 0; e < NE; e++) v[e] = nucleus_exp(v[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < NE; e++) v[e] = mass_of(nucleus_exp(v[e]), Cb);
+        }
         double ls = 0.0;
 #pragma unroll
-        for (int e = 0; e < NE; e++) ls += (double)opaque(v[e]);  // opaque: no conversion shared with the histogram
+        for (int e = 0; e < NE; e++) ls += (double)v[e];
         Skept = wave_sum(ls);
     }
 
-    // ---- draw: first index (index order) whose inclusive kept-mass prefix exceeds floor(u * Skept)
+    // ---- draw: first index (index order) whose inclusive kept-mass prefix exceeds floor(u * Skept).
+    // Per lane and sweep, the kept masses are summed left to right in fp32 (relative error below
+    // 2e-7, inside the 1e-6 band where a draw may differ from the reference's); sweep totals and
+    // prefixes add those fp32 sums exactly in double precision, and the final walk recomputes the
+    // same fp32 partial sums, so the lane found always holds the crossing.
     const double D = floor(u * Skept * gF) * gFi;
     int pick;
     {
-        // per-lane kept mass of each sweep, [lane][NS], over the histogram (whose last reads
-        // precede the ranking's wave syncs), stored two sweeps at a time to keep few doubles live
-        double* pp = reinterpret_cast<double*>(sm.u.sel.hist);
+        float* ps = reinterpret_cast<float*>(sm.u.sel.hist);  // [NS][64]: sweep-major, conflict-free
+        float ls[NS];
 #pragma unroll
-        for (int c = 0; c < NS; c += 2) {
-            double ps[2] = {0.0, 0.0};
+        for (int c = 0; c < NS; c++) {
+            float a = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const float q = v[c * 4 + k];
-                ps[k >> 2] += (double)(q >= qc ? q : 0.0f);
+            for (int j = 0; j < 4; j++) {
+                const float q = v[c * 4 + j];
+                a += q >= qc ? q : 0.0f;
             }
-            *(dbl2*)&pp[lane * NS + c] = dbl2{ps[0], ps[1]};
+            ls[c] = a;
+            ps[c * 64 + lane] = a;
         }
         wsync();
         // sweep totals: lanes 4c..4c+3 each add 16 lanes' sums of sweep c, then combine in the quad
         const int sc = lane >> 2;
         double t = 0.0;
         if (sc < NS) {
-            const int part = lane & 3;
-            const double* col = pp + part * 16 * NS + sc;
-#pragma unroll
-            for (int i = 0; i < 16; i++) t += col[((i + 4 * part) & 15) * NS];  // rotated: fewer bank conflicts
+            typedef float f4 __attribute__((ext_vector_type(4)));
+            const f4* col = reinterpret_cast<const f4*>(ps + sc * 64 + (lane & 3) * 16);
+            const f4 q0 = col[0], q1 = col[1], q2 = col[2], q3 = col[3];
+            t = (((double)q0.x + (double)q0.y) + ((double)q0.z + (double)q0.w)) +
+                (((double)q1.x + (double)q1.y) + ((double)q1.z + (double)q1.w)) +
+                ((((double)q2.x + (double)q2.y) + ((double)q2.z + (double)q2.w)) +
+                 (((double)q3.x + (double)q3.y) + ((double)q3.z + (double)q3.w)));
         }
         t = quad_sum(t);
         const double x = (lane & 3) == 0 ? t : 0.0;  // lanes past 4*NS hold 0
@@ -481,8 +594,12 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         const int sl = (int)__builtin_ctzll(sb);
         const int cs = sl >> 2;
         const double before = readlane_d(xi, sl) - readlane_d(x, sl);
-        const double mine = pp[lane * NS + cs];
-        const double li = before + wave_incl_sum(mine);
+        float mine = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NS; c++)
+            if (c == cs) mine = ls[c];
+        const double md = (double)mine;
+        const double li = before + wave_incl_sum(md);
         const uint64_t lb2 = __ballot(D < li);
         if (!lb2) return 1;
         const int L2 = (int)__builtin_ctzll(lb2);
@@ -490,12 +607,13 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
 #pragma unroll
         for (int c = 0; c < NS; c++) {
             if (c == cs) {
-                double acc = li - mine;
+                const double b0 = li - md;
+                float a = 0.0f;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const float q = opaque(v[c * 4 + j]);  // recomputed, not kept from the sums
-                    acc += (double)(q >= qc ? q : 0.0f);
-                    pick = (pick < 0 && D < acc) ? eidx(c * 4 + j) : pick;
+                    const float q = opaque(v[c * 4 + j]);
+                    a += q >= qc ? q : 0.0f;
+                    pick = (pick < 0 && D < b0 + (double)a) ? eidx(c * 4 + j) : pick;
                 }
             }
         }
