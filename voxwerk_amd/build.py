@@ -1,5 +1,6 @@
-"""Build recipe: the gfx950 HIP library, the CPU workload generator, and (for tests) the C++ facade
-test program. ``python -m voxwerk_amd.build`` or ``__graft_entry__.build()``.
+"""Build recipe: the gfx950 HIP library, the CPU workload generator, the device self-check of the
+exponentials and the native latency caller. ``python -m voxwerk_amd.build`` or
+``__graft_entry__.build()``.
 
 HIP code is compiled with -ffp-contract=off (every fp32/fp64 op of the sampler is a single IEEE
 operation, as in the reference's managed code) and with packed-FP32 instructions disabled.
@@ -9,7 +10,6 @@ from __future__ import annotations
 import os
 import shutil
 import subprocess
-import sys
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(PKG)
@@ -80,25 +80,14 @@ def build_synth() -> str:
     return out
 
 
-def build_facade_test() -> str:
-    """C++ program exercising include/voxwerk/Sampler.hpp against libvxs.so (run by a GPU test)."""
-    src = os.path.join(REPO, "tests", "cpp", "test_facade.cpp")
-    out = os.path.join(REPO, "tests", "cpp", "test_facade")
-    _run(["g++", "-O2", "-std=c++17", "-Wall", f"-I{INCLUDE}", "-o", out, src, f"-L{LIB}", "-lvxs",
-          f"-Wl,-rpath,{LIB}", "-Wl,-rpath,$ORIGIN/../../voxwerk_amd/lib"])
-    return out
-
-
-def build_all(with_tests: bool = True) -> None:
+def build_all() -> None:
     if not os.path.exists(HIPCC) and not shutil.which("hipcc"):
         raise RuntimeError("hipcc not found: a ROCm toolchain is required")
     build_synth()
     build_hip()
     build_selfcheck()
     build_latency()
-    if with_tests and os.path.exists(os.path.join(REPO, "tests", "cpp", "test_facade.cpp")):
-        build_facade_test()
 
 
 if __name__ == "__main__":
-    build_all(with_tests="--no-tests" not in sys.argv)
+    build_all()

@@ -91,7 +91,7 @@ struct vxs_ctx {
     DevBuf d_done;
     bool done_ready = false;
     HostBuf h_done;
-    int32_t done_seq = 0;
+    uint32_t done_seq = 0;  // wraps; the completion word is reset to seq - 1 before each launch
 };
 
 struct vxs_history {
@@ -347,8 +347,8 @@ int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int
         std::memcpy(hoff, res->slots, sizeof(int32_t) * rows);  // slot indices use the offsets' room
     }
     float* lg = reinterpret_cast<float*>(h + L.logits);
-    if (ld == L.ld_dev) {
-        std::memcpy(lg, logits, sizeof(float) * (size_t)rows * (size_t)ld);
+    if (ld == L.ld_dev) {  // one copy that ends at the last row's last entry (its pads are not read)
+        std::memcpy(lg, logits, sizeof(float) * ((size_t)(rows - 1) * (size_t)ld + (size_t)vocab));
     } else {
         for (int r = 0; r < rows; r++) std::memcpy(lg + (int64_t)r * L.ld_dev, logits + (int64_t)r * ld, sizeof(float) * vocab);
     }
@@ -421,9 +421,13 @@ hipError_t ensure_done(vxs_ctx* ctx, int rows, vxs::SampleArgs& a) {
     hipError_t e = ctx->h_done.reserve(sizeof(int32_t) * (16 + (size_t)rows));
     if (e != hipSuccess) return e;
     int32_t* w = static_cast<int32_t*>(ctx->h_done.p);
+    const uint32_t seq = ++ctx->done_seq;
+    // the word the host polls can never hold the new sequence before this call's kernel writes
+    // it, also in a freshly allocated (or recycled) block: the previous call's kernel has finished
+    __atomic_store_n(w, (int32_t)(seq - 1u), __ATOMIC_RELEASE);
     a.done_count = static_cast<int32_t*>(ctx->d_done.p);
     a.done_flag = w;
-    a.done_seq = ++ctx->done_seq;
+    a.done_seq = (int32_t)seq;
     a.out_ids = w + 16;
     return hipSuccess;
 }
