@@ -589,7 +589,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 logits, f64 probabilities",
+        "dtype": "fp32 logits; fp32 exp masses on a 2^-41 grid, exact fp64 sums",
         "data": "synthetic",
         "config": {
             "workload": f"{w.name}: {rows} rows x {vocab} fp32 logits, repetition penalty 1.1 over 512-id histories, "

@@ -130,6 +130,22 @@ VXS_API int vxs_sample_device(vxs_ctx* ctx, int rows, int vocab, const float* d_
                               int32_t* d_out_ids, float* d_out_logits, double* d_out_probs,
                               uint32_t flags);
 
+/*
+ * Parity/debug variant of vxs_sample_device (no counterpart in the reference): no write-back or
+ * probabilities; instead, for every row sampled by the one-wave nucleus regime (the wave path's
+ * own work: sampled rows without top-k, vocab <= 3072),
+ *   d_stats[4r + 0] = kept fraction of the probability mass (after top-p; 1 without top-p),
+ *   d_stats[4r + 1] = smallest kept probability (the top-p cut),
+ *   d_stats[4r + 2] = number of kept entries (entries whose mass is 0 on the 2^-F grid excluded),
+ *   d_stats[4r + 3] = 0,
+ * so that the nucleus is checked beyond the id; all four are NaN for every other row (greedy,
+ * exact regime, rows the one-workgroup algorithm samples). d_stats is [rows][4] fp64 device memory.
+ */
+VXS_API int vxs_sample_stats_device(vxs_ctx* ctx, int rows, int vocab, const float* d_logits, int64_t ld,
+                                    const int32_t* d_hist_off, const int32_t* d_hist_ids,
+                                    const vxs_params* d_params, int params_stride, const double* d_u,
+                                    int32_t* d_out_ids, double* d_stats, uint32_t flags);
+
 /* Wait for all work queued on the context stream. */
 VXS_API int vxs_synchronize(vxs_ctx* ctx);
 

@@ -32,8 +32,10 @@ def check_rows(ctx, logits, params, u=None, off=None, hist=None, label="", outpu
 
 
 def test_wide_workload(ctx):
+    """The full 1024-row batch the wide-vocabulary throughput figure is measured on."""
     w = workloads.workload(5)
-    b = w.generate(rows=256)
+    b = w.generate()
+    assert b.rows == 1024
     print(f"{w.name} rows={b.rows} vocab={w.vocab} digest={b.digest()[:16]}", flush=True)
     check_rows(ctx, b.logits, b.params, b.u, b.hist_off, b.hist_ids, label=w.name, outputs=False)
 
@@ -132,3 +134,22 @@ def test_wide_topp_ranks_by_probability_on_near_ties(ctx):
     p["keep_id"] = -1
     p["ban_id"] = -1
     check_rows(ctx, x, p, np.linspace(0.03, 0.97, rows), label="wide near ties")
+
+
+def test_wide_handback_next_to_ordered_rows(ctx):
+    """Rows of the wide workload's options (top-k 200, penalty, suppression) next to rows the ordered
+    pass must hand back to the general algorithm in the same workgroup: 2000 entries tied at the
+    maximum overflow its buffers, 300 tied at the k-th value exceed the exact regime's capacity."""
+    w = workloads.workload(5)
+    b = w.generate(rows=48)
+    x = b.logits.copy()
+    rng = np.random.default_rng(515)
+    vocab = w.vocab
+    for r in range(0, 48, 3):
+        cols = rng.choice(vocab - 1024, size=2000, replace=False)
+        if r % 2 == 0:
+            x[r, cols] = x[r].max() + 1.0              # 2000 ties at the maximum
+        else:
+            x[r, cols[:300]] = np.float32(x[r].max() + 0.5)  # 300 ties at the k-th value
+            x[r, cols[300:350]] = np.float32(x[r].max() + 2.0)
+    check_rows(ctx, x, b.params, b.u, b.hist_off, b.hist_ids, label="wide hand-back mix")

@@ -643,6 +643,43 @@ VXS_API int vxs_sample_device(vxs_ctx* ctx, int rows, int vocab, const float* d_
     }
 }
 
+VXS_API int vxs_sample_stats_device(vxs_ctx* ctx, int rows, int vocab, const float* d_logits, int64_t ld,
+                                    const int32_t* d_hist_off, const int32_t* d_hist_ids, const vxs_params* d_params,
+                                    int params_stride, const double* d_u, int32_t* d_out_ids, double* d_stats,
+                                    uint32_t flags) {
+    try {
+        int rc = check_shape(ctx, rows, vocab, d_logits, ld, d_params, params_stride, d_out_ids);
+        if (rc != VXS_OK) return rc;
+        if ((rc = check_flags(ctx, flags)) != VXS_OK) return rc;
+        if (!d_stats) return fail(ctx, VXS_ERR_INVALID_ARG, "stats is NULL");
+        if (rows == 0) return VXS_OK;
+        if (d_hist_off && !d_hist_ids) return fail(ctx, VXS_ERR_INVALID_ARG, "hist_ids is NULL");
+        if (params_stride > 1) return fail(ctx, VXS_ERR_INVALID_ARG, "device params_stride must be 0 or 1");
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        // all-ones bytes: every double NaN, for the rows the one-wave nucleus regime does not sample
+        VXS_HIP(ctx, hipMemsetAsync(d_stats, 0xff, sizeof(double) * 4 * (size_t)rows, ctx->stream));
+        vxs::SampleArgs a{};
+        a.rows = rows;
+        a.vocab = vocab;
+        a.ld = ld;
+        a.logits = d_logits;
+        a.hist_off = d_hist_off;
+        a.hist_ids = d_hist_ids;
+        a.params = d_params;
+        a.params_stride = params_stride;
+        a.u = d_u;
+        a.out_ids = d_out_ids;
+        a.out_stats = d_stats;
+        a.kflags = 0;
+        a.path = choose_path(flags, rows, vocab);
+        VXS_HIP(ctx, vxs::launch_sample(a, ctx->stream));
+        ctx->err.clear();
+        return VXS_OK;
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
 VXS_API int vxs_apply_repetition_penalty(vxs_ctx* ctx, int rows, int vocab, float* logits, int64_t ld,
                                          const int32_t* hist_off, const int32_t* hist_ids, float penalty) {
     try {

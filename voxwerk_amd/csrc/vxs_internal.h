@@ -33,6 +33,9 @@ struct SampleArgs {
     int32_t* out_ids;
     float* out_logits;   // optional [rows][vocab]
     double* out_probs;   // optional [rows][vocab]
+    // Optional [rows][4] (parity/debug): for a row the one-wave nucleus regime samples, its kept
+    // fraction of the mass, smallest kept probability, kept count and 0; other rows are untouched.
+    double* out_stats;
     uint32_t kflags;
     int path;            // kPathBlock or kPathQuad
     // Host-visible completion for small host calls (one workgroup per row): after its row, every

@@ -1336,7 +1336,7 @@ union QuadSmem {
     RowSmem<NC> row;
 };
 
-template <int NS, int NC>
+template <int NS, int NC, bool kStats>
 __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void sample_quad_kernel(SampleArgs a,
                                                                                                 int vec) {
     __shared__ QuadSmem<NS, NC> sm;
@@ -1346,7 +1346,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void sa
     const int r0 = blockIdx.x * kWaves;
     const int r = r0 + wv;
     int b = 0;
-    if (r < a.rows) b = wave_fast_row<NS>(a, vec, r, lane, sm.wave[wv]);
+    if (r < a.rows) b = wave_fast_row<NS, kStats>(a, vec, r, lane, sm.wave[wv]);
     if (lane == 0) back[wv] = b;
     __syncthreads();  // every wave is done with its LDS, and the flags are visible
     const int b0 = back[0], b1 = back[1], b2 = back[2], b3 = back[3];  // workgroup-uniform
@@ -1368,8 +1368,11 @@ hipError_t launch_nc(const SampleArgs& a, int vec, hipStream_t stream) {
 
 template <int NS, int NC>
 hipError_t launch_quad(const SampleArgs& a, int vec, hipStream_t stream) {
-    hipLaunchKernelGGL((sample_quad_kernel<NS, NC>), dim3((a.rows + kWaves - 1) / kWaves), dim3(kT), 0, stream, a,
-                       vec);
+    const dim3 grid((a.rows + kWaves - 1) / kWaves);
+    if (a.out_stats)  // a separate instance, so the statistics cost the sampling kernel nothing
+        hipLaunchKernelGGL((sample_quad_kernel<NS, NC, true>), grid, dim3(kT), 0, stream, a, vec);
+    else
+        hipLaunchKernelGGL((sample_quad_kernel<NS, NC, false>), grid, dim3(kT), 0, stream, a, vec);
     return hipGetLastError();
 }
 

@@ -55,6 +55,7 @@ struct Sel {
     uint64_t key[kL + 4];   // crossing-bucket entries: mass bits << 32 | index, then 4 pads
     uint64_t skey[kL];      // the same in rank order
     double ws[kL];          // their masses in rank order
+    double stot;            // total mass, kept for the optional nucleus statistics
 };
 
 // LDS ordering inside one wave.
@@ -148,7 +149,7 @@ __device__ __forceinline__ int wave_prepare(const SampleArgs& a, int r, int lane
 
 // Second half: samples row r from its loaded logits. Returns 0 when the row is done (its id
 // written) and 1, having written nothing, when it must go to the general algorithm.
-template <int NS>
+template <int NS, bool kStats>
 __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane, const vxs_params& P, WaveRow<NS>& w,
                                            WaveSmem<NS>& sm) {
     using namespace wave;
@@ -420,6 +421,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         const double lt = (double)lti * gFi;  // exact: below 2^53 units of 2^-F
         const double incl = wave_incl_sum(lt);
         const double S = readlane_d(incl, 63);
+        if constexpr (kStats) s.stot = S;
         const double T = floor(thr * S * gF) * gFi;
         const double run = incl - lt;
         const uint64_t cb = __ballot(run <= T && T - run < lt);
@@ -621,17 +623,37 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
     }
     if (pick < 0) return 1;
     if (lane == 0) a.out_ids[r] = pick;
+    if constexpr (kStats) {  // the nucleus the draw used: kept fraction, smallest kept probability, size
+        const double St = topp ? sm.u.sel.stot : Skept;
+        uint32_t kn = 0;
+        float kmin = __builtin_inff();
+#pragma unroll
+        for (int e = 0; e < NE; e++) {
+            const bool k = v[e] >= qc && v[e] > 0.0f;
+            kn += k ? 1u : 0u;
+            kmin = k ? fminf(kmin, v[e]) : kmin;
+        }
+        kn = wave_sum(kn);
+        kmin = wave_fmin(kmin);
+        if (lane == 0) {
+            double* o = a.out_stats + 4 * (int64_t)r;
+            o[0] = Skept / St;
+            o[1] = (double)kmin / St;
+            o[2] = (double)kn;
+            o[3] = 0.0;
+        }
+    }
     return 0;
 }
 
 // Samples row r (r < a.rows) with one wave: 0 when done, 1 when handed back.
-template <int NS>
+template <int NS, bool kStats>
 __device__ __forceinline__ int wave_fast_row(const SampleArgs& a, int vec, int r, int lane, WaveSmem<NS>& sm) {
     WaveRow<NS> w;
     const vxs_params P = a.params[(int64_t)r * a.params_stride];
     if (wave_prepare<NS>(a, r, lane, P, w)) return 1;
     wave_load_row<NS>(a, vec, r, lane, w);  // after the history loads: measured faster than before them
-    return wave_finish<NS>(a, r, lane, P, w, sm);
+    return wave_finish<NS, kStats>(a, r, lane, P, w, sm);
 }
 
 }  // namespace vxs
