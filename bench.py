@@ -96,6 +96,23 @@ def native_frame(rows, iters, serial=False):
     return json.loads(p.stdout.strip().splitlines()[-1])
 
 
+def native_binding_frame(frames, writeback=False):
+    """One frame of single-sequence generation as the C# binding issues it (one SelectTalker 1x3072 and
+    15 Select 1x2048, each a synchronous vxs_sample), timed per call by the native caller; None on
+    failure."""
+    import subprocess
+
+    exe = os.path.join(REPO, "voxwerk_amd", "lib", "vxs_latency")
+    if not os.path.exists(exe):
+        return None
+    p = subprocess.run([exe, "--binding-frame", str(frames)] + (["writeback"] if writeback else []),
+                       capture_output=True, text=True, timeout=300)
+    if p.returncode != 0:
+        log(f"[bench] native binding-frame probe failed: {p.stderr.strip()[:200]}")
+        return None
+    return json.loads(p.stdout.strip().splitlines()[-1])
+
+
 def measure_frame_embedding(ctx, rows: int, steps: int, hip, np) -> dict:
     """vxs_frame_embed_device over `rows` frames (16 codebooks, hidden 1024, talker and code-predictor
     tables of the real shapes, random bf16 contents, a text row added): HIP events on the context
@@ -461,6 +478,13 @@ def main() -> int:
     if native:
         log(f"[bench] talker step 1x3072 host-to-host from native code: p50 {native['p50_us']:.1f} us, "
             f"p99 {native['p99_us']:.1f} us")
+    nframes = max(1, args.latency_steps // 16)
+    bind = native_binding_frame(nframes) if args.latency_steps > 0 else None
+    bind_wb = native_binding_frame(nframes, writeback=True) if args.latency_steps > 0 else None
+    if bind_wb:
+        log(f"[bench] binding frame (SelectTalker + 15 in-place Select): p50 {bind_wb['p50_us']:.1f} us/call, "
+            f"frame p50 {bind_wb['frame_p50_us']:.1f} us; Select without write-back p50 "
+            f"{bind['select_p50_us'] if bind else float('nan'):.1f} us")
 
     cpu = None
     parity = None
@@ -608,6 +632,11 @@ def main() -> int:
             "python_p50": p50,
             "python_p99": p99,
             "workload": "talker_step 1x3072 host-to-host (host logits in, host id out)",
+            "binding_frame": dict(bind_wb, workload="one frame of TalkerGenerator.Generate as the C# binding calls "
+                                  "it: SelectTalker 1x3072 (penalty over the sequence's history, suppression, "
+                                  "draw) + 15 Select 1x2048 (top-k 50, the span written back in place), one "
+                                  "synchronous vxs_sample each, native caller",
+                                  select_without_writeback=bind) if bind_wb else None,
         },
         "roofline": {
             "bound": "hbm",

@@ -109,7 +109,8 @@ VXS_API void* vxs_get_stream(const vxs_ctx* ctx);
  *              when no row samples
  *   out_ids    [rows] sampled ids; a failing row receives its negative error code
  *   out_logits NULL or [rows][vocab]: the row as Select leaves the caller's span (after
- *              penalty, suppression, temperature and the top-k -inf mask)
+ *              penalty, suppression, temperature and the top-k -inf mask); may be `logits` itself
+ *              when ld == vocab (in place); a row that fails keeps its contents
  *   out_probs  NULL or [rows][vocab] fp64: final probabilities the draw used (parity/debug)
  * Returns VXS_OK, or the first (lowest row) error code.
  */

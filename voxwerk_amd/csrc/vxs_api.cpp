@@ -383,6 +383,7 @@ int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int
     a.path = choose_path_host(flags, rows, vocab, params, params_stride);
     if (done) {
         a.out_ids = done->out_ids;
+        if (done->out_logits) a.out_logits = done->out_logits;
         a.done_count = done->done_count;
         a.done_flag = done->done_flag;
         a.done_seq = done->done_seq;
@@ -402,15 +403,18 @@ int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int
     return VXS_OK;
 }
 
-// Host calls that can complete by polling: the one-workgroup-per-row kernel alone, ids only.
+// Host calls that can complete by polling: the one-workgroup-per-row kernel alone, ids and (up to
+// kZeroCopyMaxBytes of them) write-back logits, which the kernel then stores into coherent host memory.
 bool polled_call(int rows, int vocab, uint32_t flags, bool want_logits, bool want_probs) {
-    return !want_logits && !want_probs && vocab <= vxs::kRowResidentMaxVocab &&
-           choose_path(flags, rows, vocab) == vxs::kPathBlock && rows <= kPolledMaxRows;
+    return !want_probs && vocab <= vxs::kRowResidentMaxVocab &&
+           choose_path(flags, rows, vocab) == vxs::kPathBlock && rows <= kPolledMaxRows &&
+           (!want_logits || sizeof(float) * (size_t)rows * (size_t)vocab <= kZeroCopyMaxBytes);
 }
 
 // Completion state for a polled call of `rows` rows: the device counter (zeroed when first used and
-// after any failure) and the coherent host words the kernel writes.
-hipError_t ensure_done(vxs_ctx* ctx, int rows, vxs::SampleArgs& a) {
+// after any failure) and the coherent host words the kernel writes: the completion word, the ids
+// and, when logit_count > 0, that many write-back logits from a 256-byte boundary.
+hipError_t ensure_done(vxs_ctx* ctx, int rows, vxs::SampleArgs& a, size_t logit_count = 0) {
     if (!ctx->done_ready) {
         hipError_t e = ctx->d_done.reserve(sizeof(int32_t));
         if (e != hipSuccess) return e;
@@ -418,7 +422,8 @@ hipError_t ensure_done(vxs_ctx* ctx, int rows, vxs::SampleArgs& a) {
         ctx->done_ready = true;
     }
     ctx->h_done.flags = hipHostMallocCoherent;
-    hipError_t e = ctx->h_done.reserve(sizeof(int32_t) * (16 + (size_t)rows));
+    const size_t logits_at = align_up(sizeof(int32_t) * (16 + (size_t)rows));
+    hipError_t e = ctx->h_done.reserve(logits_at + sizeof(float) * logit_count);
     if (e != hipSuccess) return e;
     int32_t* w = static_cast<int32_t*>(ctx->h_done.p);
     const uint32_t seq = ++ctx->done_seq;
@@ -429,6 +434,7 @@ hipError_t ensure_done(vxs_ctx* ctx, int rows, vxs::SampleArgs& a) {
     a.done_flag = w;
     a.done_seq = (int32_t)seq;
     a.out_ids = w + 16;
+    a.out_logits = logit_count ? reinterpret_cast<float*>(static_cast<char*>(ctx->h_done.p) + logits_at) : nullptr;
     return hipSuccess;
 }
 
@@ -487,6 +493,31 @@ int fetch(vxs_ctx* ctx, void* dst, const void* src, size_t bytes) {
     VXS_HIP(ctx, hipMemcpyAsync(ctx->h_out.p, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
     VXS_HIP(ctx, hipStreamSynchronize(ctx->stream));
     std::memcpy(dst, ctx->h_out.p, bytes);
+    return VXS_OK;
+}
+
+// Copy the rows of `src` whose id is a token (>= 0) into `dst`; a failed row of `dst` keeps what the
+// caller had there.
+void copy_ok_rows(void* dst, const void* src, const int32_t* ids, int rows, size_t row_bytes) {
+    bool all = true;
+    for (int r = 0; r < rows && all; r++) all = ids[r] >= 0;
+    if (all) {
+        std::memcpy(dst, src, row_bytes * (size_t)rows);
+        return;
+    }
+    for (int r = 0; r < rows; r++)
+        if (ids[r] >= 0)
+            std::memcpy(static_cast<char*>(dst) + row_bytes * r, static_cast<const char*>(src) + row_bytes * r, row_bytes);
+}
+
+// fetch() of write-back rows, skipping the rows that failed.
+int fetch_ok_rows(vxs_ctx* ctx, void* dst, const void* src, const int32_t* ids, int rows, size_t row_bytes) {
+    const size_t bytes = row_bytes * (size_t)rows;
+    if (!bytes) return VXS_OK;
+    VXS_HIP(ctx, ctx->h_out.reserve(bytes));
+    VXS_HIP(ctx, hipMemcpyAsync(ctx->h_out.p, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    VXS_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    copy_ok_rows(dst, ctx->h_out.p, ids, rows, row_bytes);
     return VXS_OK;
 }
 
@@ -579,7 +610,8 @@ VXS_API int vxs_sample(vxs_ctx* ctx, int rows, int vocab, const float* logits, i
         VXS_HIP(ctx, hipSetDevice(ctx->device));
         if (polled_call(rows, vocab, flags, out_logits != nullptr, out_probs != nullptr)) {
             vxs::SampleArgs done{};
-            VXS_HIP(ctx, ensure_done(ctx, rows, done));
+            const size_t nlog = out_logits ? (size_t)rows * (size_t)vocab : 0;
+            VXS_HIP(ctx, ensure_done(ctx, rows, done, nlog));
             rc = stage_and_launch(ctx, rows, vocab, logits, ld, hist_off, hist_ids, params, params_stride, u, false,
                                   false, 0, flags, &done);
             if (rc != VXS_OK) {
@@ -588,6 +620,7 @@ VXS_API int vxs_sample(vxs_ctx* ctx, int rows, int vocab, const float* logits, i
             }
             if ((rc = wait_done(ctx, done.done_seq)) != VXS_OK) return rc;
             std::memcpy(out_ids, done.out_ids, sizeof(int32_t) * (size_t)rows);
+            if (nlog) copy_ok_rows(out_logits, done.out_logits, out_ids, rows, sizeof(float) * (size_t)vocab);
             ctx->err.clear();
             return first_row_error(ctx, out_ids, rows);
         }
@@ -595,7 +628,8 @@ VXS_API int vxs_sample(vxs_ctx* ctx, int rows, int vocab, const float* logits, i
                               out_logits != nullptr, out_probs != nullptr, 0, flags);
         if (rc != VXS_OK) return rc;
         if ((rc = fetch(ctx, out_ids, ctx->d_ids.p, sizeof(int32_t) * (size_t)rows)) != VXS_OK) return rc;
-        if (out_logits && (rc = fetch(ctx, out_logits, ctx->d_logits_out.p, sizeof(float) * (size_t)rows * vocab)) != VXS_OK)
+        if (out_logits && (rc = fetch_ok_rows(ctx, out_logits, ctx->d_logits_out.p, out_ids, rows,
+                                              sizeof(float) * (size_t)vocab)) != VXS_OK)
             return rc;
         if (out_probs && (rc = fetch(ctx, out_probs, ctx->d_probs_out.p, sizeof(double) * (size_t)rows * vocab)) != VXS_OK)
             return rc;
@@ -694,14 +728,32 @@ VXS_API int vxs_apply_repetition_penalty(vxs_ctx* ctx, int rows, int vocab, floa
         if (rows == 0 || penalty == 1.0f || !hist_off) return VXS_OK;  // Sampler.cs:27
         if ((rc = check_hist_host(ctx, rows, hist_off, hist_ids)) != VXS_OK) return rc;
         VXS_HIP(ctx, hipSetDevice(ctx->device));
+        const size_t row_bytes = sizeof(float) * (size_t)vocab;
+        if (rows <= kPolledMaxRows && vocab <= vxs::kRowResidentMaxVocab && row_bytes * rows <= kZeroCopyMaxBytes) {
+            // completes by polling, the penalised rows written straight into coherent host memory
+            vxs::SampleArgs done{};
+            VXS_HIP(ctx, ensure_done(ctx, rows, done, (size_t)rows * (size_t)vocab));
+            rc = stage_and_launch(ctx, rows, vocab, logits, ld, hist_off, hist_ids, &p, 0, nullptr, false, false,
+                                  vxs::KF_STOP_AFTER_PENALTY, VXS_FLAG_PATH_BLOCK, &done);
+            if (rc != VXS_OK) {
+                ctx->done_ready = false;
+                return rc;
+            }
+            if ((rc = wait_done(ctx, done.done_seq)) != VXS_OK) return rc;
+            ctx->err.clear();
+            if ((rc = first_row_error(ctx, done.out_ids, rows)) != VXS_OK) return rc;
+            for (int r = 0; r < rows; r++)
+                std::memcpy(logits + (int64_t)r * ld, reinterpret_cast<const char*>(done.out_logits) + row_bytes * r,
+                            row_bytes);
+            return VXS_OK;
+        }
         rc = stage_and_launch(ctx, rows, vocab, logits, ld, hist_off, hist_ids, &p, 0, nullptr, true, false,
-                              vxs::KF_STOP_AFTER_PENALTY);
+                              vxs::KF_STOP_AFTER_PENALTY, VXS_FLAG_PATH_BLOCK);
         if (rc != VXS_OK) return rc;
         VXS_HIP(ctx, ctx->h_ids.reserve(sizeof(int32_t) * (size_t)rows));
         if ((rc = fetch(ctx, ctx->h_ids.p, ctx->d_ids.p, sizeof(int32_t) * (size_t)rows)) != VXS_OK) return rc;
         ctx->err.clear();
         if ((rc = first_row_error(ctx, static_cast<int32_t*>(ctx->h_ids.p), rows)) != VXS_OK) return rc;
-        const size_t row_bytes = sizeof(float) * (size_t)vocab;
         VXS_HIP(ctx, ctx->h_out.reserve(row_bytes * rows));
         VXS_HIP(ctx, hipMemcpyAsync(ctx->h_out.p, ctx->d_logits_out.p, row_bytes * rows, hipMemcpyDeviceToHost, ctx->stream));
         VXS_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -720,15 +772,9 @@ VXS_API int vxs_argmax(vxs_ctx* ctx, int rows, int vocab, const float* logits, i
         p.rep_penalty = 1.0f;
         p.keep_id = -1;
         p.ban_id = -1;
-        int rc = check_shape(ctx, rows, vocab, logits, ld, &p, 0, out_ids);
-        if (rc != VXS_OK) return rc;
-        if (rows == 0) return VXS_OK;
-        VXS_HIP(ctx, hipSetDevice(ctx->device));
-        rc = stage_and_launch(ctx, rows, vocab, logits, ld, nullptr, nullptr, &p, 0, nullptr, false, false, 0);
-        if (rc != VXS_OK) return rc;
-        if ((rc = fetch(ctx, out_ids, ctx->d_ids.p, sizeof(int32_t) * (size_t)rows)) != VXS_OK) return rc;
-        ctx->err.clear();
-        return first_row_error(ctx, out_ids, rows);
+        // a greedy row of vxs_sample: no history, no draw (polled completion for small calls)
+        return vxs_sample(ctx, rows, vocab, logits, ld, nullptr, nullptr, &p, 0, nullptr, out_ids, nullptr, nullptr,
+                          VXS_FLAG_NONE);
     } catch (...) {
         return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
     }

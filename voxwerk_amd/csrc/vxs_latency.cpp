@@ -6,6 +6,14 @@
 // rows*hist_len int32 history ids, rows vxs_params, rows float64 uniforms.
 // output: one JSON line {"p50_us": .., "p99_us": .., "iters": .., "id0": ..}
 //
+// usage: vxs_latency --binding-frame <frames> [writeback]
+// One frame of single-sequence generation (TalkerGenerator.Generate, TalkerGenerator.cs:241-272) as the
+// C# binding issues it: one SelectTalker (1 x 3072: penalty over the sequence's history, suppression of
+// the last 1024 ids except EOS, EOS ban for the first two frames, draw) and 15 Select (1 x 2048, top-k
+// 50, T 0.9, draw), each one synchronous vxs_sample. With "writeback", Select also writes the row back
+// into the caller's span (the reference's in-place Select); by default it does not, as no caller reads
+// the span after Select. Output {"p50_us": per call, "talker_p50_us", "select_p50_us", "frame_p50_us", ..}.
+//
 // usage: vxs_latency --frame <rows> <iterations> [serial]
 // One frame step of batched generation (TalkerGenerator.GenerateBatch, TalkerGenerator.cs:362-426)
 // over `rows` sequences: the talker stage (rows x 3072, penalty over resident histories, suppression,
@@ -113,16 +121,85 @@ int frame_mode(int rows, int iters, bool serial) {
     return 0;
 }
 
+int binding_frame_mode(int frames, bool writeback) {
+    Rng rng{0xD1B54A32D192ED03ULL};
+    constexpr int kRot = 8;  // distinct synthetic rows per stage, used in turn
+    std::vector<float> talker((size_t)kRot * kTalkerVocab), cp((size_t)kRot * kCpVocab), span(kCpVocab);
+    for (float& x : talker) x = (float)(6.0 * rng.next() - 3.0);
+    for (float& x : cp) x = (float)(6.0 * rng.next() - 3.0);
+    const vxs_params cpp{1, 50, 1.0f, 0.9f, 1.0f, 0, 0, -1, -1};
+    vxs_ctx* ctx = nullptr;
+    if (vxs_create(&ctx, 0, 64, kTalkerVocab, 1 << 16) != VXS_OK) {
+        std::fprintf(stderr, "vxs_create failed\n");
+        return 1;
+    }
+    std::vector<int32_t> history;
+    std::vector<double> tt, ts, tf;
+    const int warm = 50;
+    int rc = VXS_OK;
+    for (int f = 0; f < warm + frames && rc == VXS_OK; f++) {
+        const int t = f % 256;  // a sequence of 256 frames, then a new one
+        if (t == 0) history.clear();
+        const vxs_params tp{1, 50, 1.0f, 0.9f, 1.05f, kTalkerVocab - 1024, kTalkerVocab, kEos, t < 2 ? kEos : -1};
+        const auto f0 = std::chrono::steady_clock::now();
+        const int32_t off[2] = {0, (int32_t)history.size()};
+        double u = rng.next();
+        int32_t id = 0;
+        rc = vxs_sample(ctx, 1, kTalkerVocab, talker.data() + (size_t)(f % kRot) * kTalkerVocab, kTalkerVocab, off,
+                        history.data(), &tp, 0, &u, &id, nullptr, nullptr, 0);
+        const auto f1 = std::chrono::steady_clock::now();
+        if (rc != VXS_OK) break;
+        history.push_back(id);
+        if (f >= warm) tt.push_back(std::chrono::duration<double, std::micro>(f1 - f0).count());
+        for (int g = 1; g < kGroups && rc == VXS_OK; g++) {
+            // the caller's span: the head writes fresh logits into it before every Select
+            std::memcpy(span.data(), cp.data() + (size_t)((f + g) % kRot) * kCpVocab, sizeof(float) * kCpVocab);
+            u = rng.next();
+            const auto s0 = std::chrono::steady_clock::now();
+            rc = vxs_sample(ctx, 1, kCpVocab, span.data(), kCpVocab, nullptr, nullptr, &cpp, 0, &u, &id,
+                            writeback ? span.data() : nullptr, nullptr, 0);
+            if (f >= warm)
+                ts.push_back(std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - s0).count());
+        }
+        if (f >= warm && rc == VXS_OK) {
+            double frame = tt.back();
+            for (int g = 1; g < kGroups; g++) frame += ts[ts.size() - kGroups + g];
+            tf.push_back(frame);
+        }
+    }
+    if (rc != VXS_OK) std::fprintf(stderr, "sampling failed: %s\n", vxs_last_error(ctx));
+    vxs_destroy(ctx);
+    if (rc != VXS_OK) return 1;
+    std::vector<double> all(tt);
+    all.insert(all.end(), ts.begin(), ts.end());
+    auto pct = [](std::vector<double>& v, double q) {
+        std::sort(v.begin(), v.end());
+        return v[std::min(v.size() - 1, (size_t)(v.size() * q))];
+    };
+    std::printf("{\"p50_us\": %.2f, \"p99_us\": %.2f, \"talker_p50_us\": %.2f, \"select_p50_us\": %.2f, "
+                "\"select_p99_us\": %.2f, \"frame_p50_us\": %.2f, \"frames\": %d, \"calls_per_frame\": %d, "
+                "\"writeback\": %s}\n",
+                pct(all, 0.5), pct(all, 0.99), pct(tt, 0.5), pct(ts, 0.5), pct(ts, 0.99), pct(tf, 0.5), frames, kGroups,
+                writeback ? "true" : "false");
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
+    if (argc >= 3 && std::strcmp(argv[1], "--binding-frame") == 0) {
+        const int frames = std::atoi(argv[2]);
+        if (frames <= 0) return 2;
+        return binding_frame_mode(frames, argc >= 4 && std::strcmp(argv[3], "writeback") == 0);
+    }
     if (argc >= 4 && std::strcmp(argv[1], "--frame") == 0) {
         const int rows = std::atoi(argv[2]), iters = std::atoi(argv[3]);
         if (rows <= 0 || iters <= 0) return 2;
         return frame_mode(rows, iters, argc >= 5 && std::strcmp(argv[4], "serial") == 0);
     }
     if (argc < 3) {
-        std::fprintf(stderr, "usage: %s <input file> <iterations> | --frame <rows> <iterations> [serial]\n", argv[0]);
+        std::fprintf(stderr, "usage: %s <input file> <iterations> | --frame <rows> <iterations> [serial] | --binding-frame <frames> "
+                     "[writeback]\n", argv[0]);
         return 2;
     }
     std::FILE* f = std::fopen(argv[1], "rb");

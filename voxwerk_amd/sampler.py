@@ -260,9 +260,11 @@ class Context:
     def sample(self, logits: np.ndarray, params: np.ndarray, u: Optional[np.ndarray] = None,
                hist_off: Optional[np.ndarray] = None, hist_ids: Optional[np.ndarray] = None,
                want_logits: bool = False, want_probs: bool = False, raise_on_error: bool = True,
-               path: str = "auto"):
+               path: str = "auto", logits_out: Optional[np.ndarray] = None):
         """Sample every row of `logits` [rows, vocab] (host). `params`: one PARAMS_DTYPE record
-        (broadcast) or one per row. Returns ids (and the write-back logits / probabilities)."""
+        (broadcast) or one per row. Returns ids (and the write-back logits / probabilities).
+        `logits_out` (float32 [rows, vocab], C-contiguous) receives the write-back instead of a new
+        array; a row that fails keeps what it held."""
         logits = np.ascontiguousarray(logits, dtype=np.float32)
         if logits.ndim == 1:
             logits = logits.reshape(1, -1)
@@ -279,7 +281,13 @@ class Context:
             hist_off = np.ascontiguousarray(hist_off, dtype=np.int32)
             hist_ids = np.ascontiguousarray(hist_ids if hist_ids is not None else np.zeros(0, np.int32), dtype=np.int32)
         ids = np.empty(rows, dtype=np.int32)
-        out_logits = np.empty((rows, vocab), dtype=np.float32) if want_logits else None
+        if logits_out is not None:
+            if (logits_out.dtype != np.float32 or logits_out.shape != (rows, vocab)
+                    or not logits_out.flags.c_contiguous):
+                raise ValueError("logits_out must be a C-contiguous float32 [rows, vocab] array")
+            want_logits = True
+        out_logits = (logits_out if logits_out is not None else np.empty((rows, vocab), dtype=np.float32)) \
+            if want_logits else None
         out_probs = np.empty((rows, vocab), dtype=np.float64) if want_probs else None
         rc = self._lib.vxs_sample(self._h, rows, vocab, ptr(logits), vocab, ptr(hist_off), ptr(hist_ids),
                                   ptr(params), stride, ptr(u), ptr(ids), ptr(out_logits), ptr(out_probs),
