@@ -43,6 +43,8 @@ def load() -> ctypes.CDLL:
         lib.vxs_oracle_apply_penalty.argtypes = [c_int, c_int, c_void_p, c_int64, c_void_p, c_void_p, c_float]
         lib.vxs_oracle_argmax.restype = c_int
         lib.vxs_oracle_argmax.argtypes = [c_int, c_void_p]
+        lib.vxs_oracle_random_stream.restype = c_int
+        lib.vxs_oracle_random_stream.argtypes = [c_int32, c_int64, c_void_p, c_void_p]
         _lib = lib
     return _lib
 
@@ -82,6 +84,14 @@ def apply_penalty(logits, hist_off, hist_ids, penalty) -> int:
     return lib.vxs_oracle_apply_penalty(x.shape[0], x.shape[1], _p(x), x.shape[1],
                                         _p(np.ascontiguousarray(hist_off, np.int32)),
                                         _p(np.ascontiguousarray(hist_ids, np.int32)), float(np.float32(penalty)))
+
+
+def random_stream(seed: int, n: int):
+    """The first n draws of .NET's new Random(seed): (Next() values int32, NextDouble() values)."""
+    samples = np.empty(n, np.int32)
+    doubles = np.empty(n, np.float64)
+    assert load().vxs_oracle_random_stream(int(seed), int(n), _p(samples), _p(doubles)) == 0
+    return samples, doubles
 
 
 def argmax(x) -> int:

@@ -34,6 +34,19 @@ int vxs_oracle_sample(int rows, int vocab, const float* logits, int64_t ld, cons
 int vxs_oracle_apply_penalty(int rows, int vocab, float* logits, int64_t ld, const int32_t* hist_off,
                              const int32_t* hist_ids, float penalty);
 
+/* .NET's seeded System.Random (vxs_oracle_random.c): the 56-entry table and its two cursors. */
+typedef struct vxs_oracle_random {
+    int32_t table[56];
+    int next, nextp;
+} vxs_oracle_random;
+
+void vxs_oracle_random_seed(vxs_oracle_random* g, int32_t seed);    /* new Random(seed)      */
+int32_t vxs_oracle_random_sample(vxs_oracle_random* g);              /* InternalSample()/Next() */
+double vxs_oracle_random_next_double(vxs_oracle_random* g);          /* NextDouble()          */
+/* The first n draws of new Random(seed): Next() values into samples and NextDouble() values into
+ * doubles (either may be NULL). */
+int vxs_oracle_random_stream(int32_t seed, int64_t n, int32_t* samples, double* doubles);
+
 #ifdef __cplusplus
 }
 #endif

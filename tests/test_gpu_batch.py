@@ -167,20 +167,26 @@ def _i32(x):
 
 
 def test_device_generators_match_dotnet_random(ctx):
-    """The slot generators drawn on the device reproduce DotNetRandom (the host restatement of .NET's
-    seeded System.Random) bit for bit, for new Random(seed) and new Random(seed + 1)."""
+    """The slot generators drawn on the device reproduce the oracle's C restatement of .NET's seeded
+    System.Random and the host DotNetRandom bit for bit, for new Random(seed) and new Random(seed + 1),
+    over 20000 draws per generator taken in uneven pieces, wrapping seeds included."""
+    from oracle import ref
     from voxwerk_amd.sampler import DotNetRandom
 
-    seeds = [0, 1, 42, 161803399, 10**9, 2**31 - 1, -(2**31), -7, 2_000_000_000, 123456789]
+    seeds = [0, 1, 42, 161803397, 161803398, 161803399, 10**9, 2**31 - 1, -(2**31), -(2**31) + 1, -7,
+             2_000_000_000, 123456789, -987654321]
+    n = 20000
     with ctx.history(len(seeds), 4) as store:
         for s, seed in enumerate(seeds):
             store.seed(s, seed)
         for s, seed in enumerate(seeds):
             for stream, sd in (("talker", seed), ("sub", _i32(seed + 1))):
-                host = DotNetRandom(sd)
-                want = np.array([host.NextDouble() for _ in range(700)])
-                got = np.concatenate([store.draw(s, stream, 200), store.draw(s, stream, 500)])
+                want = ref.random_stream(sd, n)[1]
+                got = np.concatenate([store.draw(s, stream, k) for k in (1, 199, 500, 4300, n - 5000)])
                 assert np.array_equal(got.view(np.uint64), want.view(np.uint64)), (seed, stream)
+                host = DotNetRandom(sd)
+                first = np.array([host.NextDouble() for _ in range(700)])
+                assert np.array_equal(first.view(np.uint64), want[:700].view(np.uint64)), (seed, stream)
 
 
 def test_batch_draws_uniforms_on_device(ctx):

@@ -82,7 +82,7 @@ struct vxs_ctx {
     hipStream_t stream = nullptr;
     std::string err;
     DevBuf d_in, d_ids, d_logits_out, d_probs_out;
-    DevBuf d_draw;   // uniforms drawn on the device for a batch call (and vxs_history_draw)
+    DevBuf d_draw;   // uniforms drawn on the device by vxs_history_draw
     HostBuf h_in, h_ids, h_out;  // h_in is coherent: polled calls' kernels read it in place
     void* h_in_dev = nullptr;    // device address of h_in.p
     void* h_in_dev_of = nullptr;  // the h_in.p that h_in_dev belongs to
@@ -101,6 +101,7 @@ struct vxs_history {
     int32_t* ids = nullptr;  // [slots][cap]
     int32_t* len = nullptr;  // [slots]
     int32_t* rng = nullptr;  // [slots][2][kRngWords]: talker and code-predictor generators
+    vxs::StoreDesc* desc = nullptr;  // the three pointers and the shape, in device memory
     std::vector<uint8_t> seeded;  // host record of vxs_history_seed per slot
 };
 
@@ -237,7 +238,7 @@ int check_flags(vxs_ctx* ctx, uint32_t flags) {
 }
 
 // A call whose histories live in a resident store: host slot indices (staged with the inputs),
-// whether to append, and the completion words of a polled call (published by the append kernel).
+// whether to append, the generator stream, and the completion words of a polled call.
 struct ResidentCall {
     const vxs_history* store = nullptr;
     const int32_t* slots = nullptr;
@@ -284,45 +285,18 @@ void dotnet_seed(int32_t seed, int32_t* st) {
     st[57] = 21;
 }
 
-// Row histories of a resident call, and the append kernel that follows its sampler.
-void set_resident(vxs::SampleArgs& a, const vxs_history* h, const int32_t* d_slots) {
+// Row histories of a resident call: the sampler reads each row's slot and ends its step itself
+// (draw from the slot's generator when rng_stream >= 0, append when `append`, slot check).
+void set_resident(vxs::SampleArgs& a, const vxs_history* h, const int32_t* d_slots, int append, int rng_stream) {
     a.hist_off = nullptr;
     a.hist_ids = h->ids;
     a.hist_slot = d_slots;
     a.hist_len = h->len;
     a.hist_cap = h->cap;
     a.hist_slots = h->slots;
-}
-
-vxs::AppendArgs append_args(const vxs::SampleArgs& a, const vxs_history* h, int append) {
-    vxs::AppendArgs b{};
-    b.rows = a.rows;
-    b.slots = h->slots;
-    b.cap = h->cap;
-    b.append = append;
-    b.slot = a.hist_slot;
-    b.len = h->len;
-    b.ids = h->ids;
-    b.out_ids = a.out_ids;
-    return b;
-}
-
-// Queue the draw of one uniform per sampled row from its slot's generator into ctx->d_draw, and
-// point the sampler's uniforms there.
-hipError_t draw_for(vxs_ctx* ctx, vxs::SampleArgs& a, const vxs_history* h, int stream) {
-    hipError_t e = ctx->d_draw.reserve(sizeof(double) * (size_t)a.rows);
-    if (e != hipSuccess) return e;
-    vxs::DrawArgs b{};
-    b.rows = a.rows;
-    b.slots = h->slots;
-    b.stream = stream;
-    b.slot = a.hist_slot;
-    b.params = a.params;
-    b.params_stride = a.params_stride;
-    b.rng = h->rng;
-    b.u = static_cast<double*>(ctx->d_draw.p);
-    a.u = b.u;
-    return vxs::launch_draw_uniforms(b, ctx->stream);
+    a.store = h->desc;
+    if (append) a.kflags |= vxs::KF_APPEND;
+    if (rng_stream >= 0) a.kflags |= vxs::KF_RNG | (rng_stream == 1 ? vxs::KF_RNG_SUB : 0u);
 }
 
 // Stage inputs and launch. On success the kernels are queued on ctx->stream.
@@ -381,6 +355,7 @@ int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int
     a.out_probs = want_probs ? static_cast<double*>(ctx->d_probs_out.p) : nullptr;
     a.kflags = kflags;
     a.path = choose_path_host(flags, rows, vocab, params, params_stride);
+    if (res && res->done) done = res->done;
     if (done) {
         a.out_ids = done->out_ids;
         if (done->out_logits) a.out_logits = done->out_logits;
@@ -388,18 +363,8 @@ int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int
         a.done_flag = done->done_flag;
         a.done_seq = done->done_seq;
     }
-    if (res) set_resident(a, res->store, reinterpret_cast<const int32_t*>(d + L.hoff));
-    if (res && res->rng_stream >= 0) VXS_HIP(ctx, draw_for(ctx, a, res->store, res->rng_stream));
+    if (res) set_resident(a, res->store, reinterpret_cast<const int32_t*>(d + L.hoff), res->append, res->rng_stream);
     VXS_HIP(ctx, vxs::launch_sample(a, ctx->stream));
-    if (res) {
-        vxs::AppendArgs b = append_args(a, res->store, res->append);
-        if (res->done) {
-            b.host_ids = res->done->out_ids;
-            b.done_flag = res->done->done_flag;
-            b.done_seq = res->done->done_seq;
-        }
-        VXS_HIP(ctx, vxs::launch_history_append(b, ctx->stream));
-    }
     return VXS_OK;
 }
 
@@ -805,6 +770,12 @@ VXS_API int vxs_history_create(vxs_ctx* ctx, int slots, int cap, vxs_history** o
         if (e == hipSuccess) e = hipMalloc(&h->rng, rng_bytes);
         if (e == hipSuccess) e = hipMemsetAsync(h->len, 0, sizeof(int32_t) * (size_t)slots, ctx->stream);
         if (e == hipSuccess) e = hipMemsetAsync(h->rng, 0, rng_bytes, ctx->stream);
+        if (e == hipSuccess) e = hipMalloc(&h->desc, sizeof(vxs::StoreDesc));
+        if (e == hipSuccess) {
+            const vxs::StoreDesc d{h->ids, h->len, h->rng, cap, slots};
+            e = hipMemcpyAsync(h->desc, &d, sizeof d, hipMemcpyHostToDevice, ctx->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        }
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
         if (e != hipSuccess) {
             vxs_history_destroy(h);
@@ -824,6 +795,7 @@ VXS_API void vxs_history_destroy(vxs_history* h) {
     if (h->ids) (void)hipFree(h->ids);
     if (h->len) (void)hipFree(h->len);
     if (h->rng) (void)hipFree(h->rng);
+    if (h->desc) (void)hipFree(h->desc);
     delete h;
 }
 
@@ -985,16 +957,14 @@ VXS_API int vxs_sample_batch_device(vxs_ctx* ctx, vxs_history* h, int rows, int 
         a.vocab = vocab;
         a.ld = ld;
         a.logits = d_logits;
-        set_resident(a, h, d_slots);
         a.params = d_params;
         a.params_stride = params_stride;
         a.u = d_u;
         a.out_ids = d_out_ids;
         a.kflags = 0;
         a.path = choose_path(flags, rows, vocab);
-        if (rng_stream_of(flags) >= 0) VXS_HIP(ctx, draw_for(ctx, a, h, rng_stream_of(flags)));
+        set_resident(a, h, d_slots, append != 0, rng_stream_of(flags));
         VXS_HIP(ctx, vxs::launch_sample(a, ctx->stream));
-        VXS_HIP(ctx, vxs::launch_history_append(append_args(a, h, append != 0), ctx->stream));
         ctx->err.clear();
         return VXS_OK;
     } catch (...) {

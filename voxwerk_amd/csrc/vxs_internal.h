@@ -11,6 +11,19 @@ namespace vxs {
 // Kernel-side flags (not part of the public ABI).
 enum : uint32_t {
     KF_STOP_AFTER_PENALTY = 1u,  // apply penalty (+ write-back) only: ApplyRepetitionPenalty
+    KF_APPEND = 2u,              // resident store: append each sampled id to its row's slot
+    KF_RNG = 4u,                 // resident store: draw the uniforms from the slots' generators
+    KF_RNG_SUB = 8u,             //   the code predictor's (else the talker's)
+};
+
+// A resident store as the kernels see it (vxs_history, one copy in device memory per store):
+// ids [slots][cap], lengths [slots], generators [slots][2][kRngWords].
+struct StoreDesc {
+    int32_t* ids;
+    int32_t* len;
+    int32_t* rng;
+    int cap;
+    int slots;
 };
 
 struct SampleArgs {
@@ -22,11 +35,16 @@ struct SampleArgs {
     const int32_t* hist_ids;
     // Resident histories (vxs_history), used instead of hist_off when hist_len is set: row r reads
     // slot s = hist_slot[r], the ids hist_ids[s * hist_cap, s * hist_cap + min(hist_len[s], hist_cap)).
-    // A slot outside [0, hist_slots) reads as empty; the append kernel then fails the row.
+    // A slot outside [0, hist_slots) reads as empty, and put_id then fails the row.
     const int32_t* hist_slot;
     const int32_t* hist_len;
     int hist_cap;
     int hist_slots;
+    // With a resident store (`store`, in device memory), the row's step ends in the kernel
+    // (put_id): with KF_APPEND the slot takes the sampled id, and with KF_RNG a sampled row's
+    // uniform is the next NextDouble() of generator 2 * slot + (KF_RNG_SUB ? 1 : 0) instead of u[r]
+    // (read by row_uniform, advanced once by put_id).
+    const struct StoreDesc* store;
     const vxs_params* params;
     int params_stride;
     const double* u;
@@ -77,42 +95,82 @@ __device__ __forceinline__ HistRange history_range(const SampleArgs& a, int r) {
     return {h0, h0 + min(max(n, 0), a.hist_cap)};
 }
 
-// Resident-history step after a sampling launch: per row, fail a row whose slot lies outside
-// [0, slots); when `append`, add a sampled id (>= 0) to its slot, or fail the row with
-// VXS_ERR_HISTORY_FULL when the slot holds `cap` ids. With `host_ids`, one workgroup handles every
-// row, copies the final ids there and then stores `done_seq` to `done_flag` (a host-polled call).
-struct AppendArgs {
-    int rows;
-    int slots;
-    int cap;
-    int append;
-    const int32_t* slot;
-    int32_t* len;
-    int32_t* ids;
-    int32_t* out_ids;
-    int32_t* host_ids;
-    int32_t* done_flag;
-    int32_t done_seq;
-};
-
 // Per-sequence generators of a resident store: .NET's seeded System.Random state, kRngWords int32
 // per generator (SeedArray[1..55] at [1..55], inext at [56], inextp at [57]), two per slot (the
 // talker's at 2s, the code predictor's at 2s + 1).
 constexpr int kRngWords = 64;
 
-// Uniforms of a batch call drawn on the device: row r takes the next NextDouble() of generator
-// 2 * slot[r] + stream when it samples (params do_sample), else 0 and no draw (Sampler.cs:37,77).
-// A slot outside [0, slots) gets 0 (the append kernel fails the row).
-struct DrawArgs {
-    int rows;
-    int slots;
-    int stream;
-    const int32_t* slot;
-    const vxs_params* params;
-    int params_stride;
-    int32_t* rng;
-    double* u;
+// The next InternalSample() of generator state `st` (Random.InternalSample with C#'s wrapping int
+// arithmetic): the value and the table slot it replaces. Nothing is written.
+struct RngStep {
+    int32_t v;
+    int i, j;
 };
+__device__ __forceinline__ RngStep rng_peek(const int32_t* st) {
+    constexpr int32_t kMbig = 0x7FFFFFFF;
+    int i = st[56] + 1;
+    if (i >= 56) i = 1;
+    int j = st[57] + 1;
+    if (j >= 56) j = 1;
+    int32_t v = (int32_t)((uint32_t)st[i] - (uint32_t)st[j]);
+    if (v == kMbig) v--;
+    if (v < 0) v = (int32_t)((uint32_t)v + (uint32_t)kMbig);
+    return {v, i, j};
+}
+__device__ __forceinline__ void rng_commit(int32_t* st, const RngStep& t) {
+    st[t.i] = t.v;
+    st[56] = t.i;
+    st[57] = t.j;
+}
+// NextDouble() = InternalSample() * (1.0 / int.MaxValue) (Sampler.cs:77).
+__device__ __forceinline__ double rng_double(int32_t v) { return (double)v * (1.0 / 2147483647.0); }
+
+// The uniform row r's draw uses: u[r], or with a resident store's generators the next NextDouble()
+// of its slot's generator, read without advancing it (put_id advances it once for the row). Any
+// number of threads may call it before the row's put_id. 0 for a slot outside the store.
+__device__ __forceinline__ int32_t* slot_rng(const SampleArgs& a, const StoreDesc& d, int s) {
+    return d.rng + ((int64_t)s * 2 + ((a.kflags & KF_RNG_SUB) ? 1 : 0)) * kRngWords;
+}
+__device__ __forceinline__ double row_uniform(const SampleArgs& a, int r) {
+    if (a.kflags & KF_RNG) {
+        const StoreDesc d = *a.store;
+        const int s = a.hist_slot[r];
+        if ((unsigned)s >= (unsigned)d.slots) return 0.0;
+        return rng_double(rng_peek(slot_rng(a, d, s)).v);
+    }
+    return a.u ? a.u[r] : 0.0;
+}
+
+// The one store of row r's result, by one thread after every thread of the row has taken its
+// uniform. With a resident store it also ends the row's step (the order of the batched
+// generator's loop, TalkerGenerator.cs:369-374): a row whose slot lies outside the store fails with
+// VXS_ERR_INVALID_ARG; a sampled row advances its slot's generator (one NextDouble per sampled
+// Select, whatever the outcome, Sampler.cs:77); with `append` a sampled id joins the slot's
+// history (History.Add), or the row fails with VXS_ERR_HISTORY_FULL when the slot is full.
+__device__ __forceinline__ void put_id(const SampleArgs& a, int r, int id) {
+    if (a.store) {  // the descriptor is read here, at the row's end
+        const StoreDesc d = *a.store;
+        const int s = a.hist_slot[r];
+        if ((unsigned)s >= (unsigned)d.slots) {
+            id = VXS_ERR_INVALID_ARG;
+        } else {
+            if ((a.kflags & KF_RNG) && a.params[(int64_t)r * a.params_stride].do_sample) {
+                int32_t* st = slot_rng(a, d, s);
+                rng_commit(st, rng_peek(st));
+            }
+            if ((a.kflags & KF_APPEND) && id >= 0) {
+                const int n = d.len[s];
+                if ((unsigned)n >= (unsigned)d.cap) {
+                    id = VXS_ERR_HISTORY_FULL;
+                } else {
+                    d.ids[(int64_t)s * d.cap + n] = id;
+                    d.len[s] = n + 1;
+                }
+            }
+        }
+    }
+    a.out_ids[r] = id;
+}
 
 // Embedding of sampled ids (vxs_embed.hip). `vec`: hidden % 4 == 0 and every base pointer and
 // leading dimension allows 8-byte bf16 and 16-byte fp32 accesses. status[r] = 0 or
@@ -157,8 +215,6 @@ hipError_t launch_frame_embed(const FrameEmbedArgs& a, hipStream_t stream);
 // Enqueue the sampler on `stream`. Returns hipSuccess or the launch error.
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream);
 hipError_t launch_sample_wide(const SampleArgs& a, hipStream_t stream);
-hipError_t launch_history_append(const AppendArgs& a, hipStream_t stream);
-hipError_t launch_draw_uniforms(const DrawArgs& a, hipStream_t stream);
 // n successive NextDouble() of one generator into out[0..n) (one thread; a check and debug aid).
 hipError_t launch_draw_sequence(int32_t* state, int n, double* out, hipStream_t stream);
 

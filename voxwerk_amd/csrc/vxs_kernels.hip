@@ -592,7 +592,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
                 if (hb + k * kT + g.t < h1) own(id[k]);
         }
         if (g.any(bad, kSiteErr)) {
-            if (g.t == 0) a.out_ids[r] = VXS_ERR_ID_OUT_OF_RANGE;
+            if (g.t == 0) put_id(a, r, VXS_ERR_ID_OUT_OF_RANGE);
             return;
         }
 #pragma unroll
@@ -617,7 +617,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
 
     if (a.kflags & KF_STOP_AFTER_PENALTY) {
         write_logits();
-        if (g.t == 0) a.out_ids[r] = 0;
+        if (g.t == 0) put_id(a, r, 0);
         return;
     }
 
@@ -661,7 +661,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
                 bi = oi;
             }
         }
-        if (g.t == 0) a.out_ids[r] = anynan ? VXS_ERR_NONFINITE : bi;
+        if (g.t == 0) put_id(a, r, anynan ? VXS_ERR_NONFINITE : bi);
         write_logits();
         if (prow)
 #pragma unroll
@@ -713,7 +713,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
             anybad |= g.slot[kSiteStat0 + 3][i];
         }
         if (anybad) {
-            if (g.t == 0) a.out_ids[r] = VXS_ERR_NONFINITE;
+            if (g.t == 0) put_id(a, r, VXS_ERR_NONFINITE);
             return;
         }
         cnt = (uint32_t)V;
@@ -727,7 +727,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
 
     // every entry is -inf: p = 0/0 everywhere and the reference's draw returns the last id
     if (cnt == 0) {
-        if (g.t == 0) a.out_ids[r] = V - 1;
+        if (g.t == 0) put_id(a, r, V - 1);
         write_logits();
         if (prow)
 #pragma unroll
@@ -868,7 +868,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
     write_logits();
 
     const float m = mx;
-    const double u = a.u ? a.u[r] : 0.0;
+    const double u = row_uniform(a, r);
 
     if (cnt <= (uint32_t)kCandMax) {
         // ================= exact regime: the reference's sequential fp64 arithmetic =================
@@ -988,7 +988,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
         }
         if (g.wv == 0) {  // inverse-CDF draw in index order                              :77-87
             const int pick = wave_draw(ex.cp, ex.ci, n, u, ex.pre, g.lane);
-            if (g.lane == 0) a.out_ids[r] = pick;
+            if (g.lane == 0) put_id(a, r, pick);
         }
         if (prow)
             for (int j = g.t; j < n; j += kT) prow[ex.ci[j]] = ex.cp[j];
@@ -1290,7 +1290,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
         pick = g.imax(li, kSiteLast);
         if (pick < 0) pick = 0;
     }
-    if (g.t == 0) a.out_ids[r] = pick;
+    if (g.t == 0) put_id(a, r, pick);
     if (prow) {
         double se = 0.0;
 #pragma unroll

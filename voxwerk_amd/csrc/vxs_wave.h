@@ -128,7 +128,8 @@ __device__ __forceinline__ void wave_load_row(const SampleArgs& a, int vec, int 
 template <int NS>
 __device__ __forceinline__ int wave_prepare(const SampleArgs& a, int r, int lane, const vxs_params& P, WaveRow<NS>& w) {
     using namespace wave;
-    if (a.out_logits || a.out_probs || (a.kflags & KF_STOP_AFTER_PENALTY)) return 1;
+    // outputs, the penalty alone and resident stores (whose step ends in put_id) take the general path
+    if (a.out_logits || a.out_probs || (a.kflags & KF_STOP_AFTER_PENALTY) || a.store) return 1;
     if (P.do_sample && P.top_k > 0 && P.top_k < a.vocab) return 1;
     const bool pen_on = P.rep_penalty != 1.0f && has_history(a);
     HistRange hr{0, 0};

@@ -368,7 +368,7 @@ __device__ __forceinline__ bool build_bitmap(const BlkW& g, const SampleArgs& a,
         }
     }
     if (g.any(bad)) {
-        if (g.t == 0) a.out_ids[r] = VXS_ERR_ID_OUT_OF_RANGE;
+        if (g.t == 0) put_id(a, r, VXS_ERR_ID_OUT_OF_RANGE);
         return false;
     }
     return true;
@@ -400,7 +400,7 @@ __device__ __forceinline__ void wide_general_row(const SampleArgs& a, int vec, i
         P1.keep = P1.ban = -1;
         P1.invT = 1.0f;
         for_row(xrow, V, vec, g.t, P1, [&](int i, float x) { orow[i] = x; });
-        if (g.t == 0) a.out_ids[r] = 0;
+        if (g.t == 0) put_id(a, r, 0);
         return;
     }
     X.sb = max(P.supp_begin, 0);
@@ -566,7 +566,7 @@ __device__ __forceinline__ void wide_general_row(const SampleArgs& a, int vec, i
     const bool huge = xmin < -1.0e37f;  // a deferred penalty might overflow such a value to -inf
     if (g.lane == 0) s.wcnt[g.wv] = collect ? wn : -1;
     if (g.any(bad)) {
-        if (g.t == 0) a.out_ids[r] = VXS_ERR_NONFINITE;
+        if (g.t == 0) put_id(a, r, VXS_ERR_NONFINITE);
         return;
     }
     if (greedy) {
@@ -589,7 +589,7 @@ __device__ __forceinline__ void wide_general_row(const SampleArgs& a, int vec, i
                 besti = oi;
             }
         }
-        if (g.t == 0) a.out_ids[r] = (int)besti;
+        if (g.t == 0) put_id(a, r, (int)besti);
         if (orow) for_row(xrow, V, vec, g.t, X, [&](int i, float x) { orow[i] = x; });
         if (prow)
             for (int i = g.t; i < V; i += kTW) prow[i] = 0.0;
@@ -612,9 +612,9 @@ __device__ __forceinline__ void wide_general_row(const SampleArgs& a, int vec, i
         mx = key2f(g.umax(f2key(wave_fmax(m2))));
         cnt = g.usum(c2);
     }
-    const double u = a.u ? a.u[r] : 0.0;
+    const double u = row_uniform(a, r);
     if (cnt == 0) {  // every entry -inf: the reference's draw returns the last id
-        if (g.t == 0) a.out_ids[r] = V - 1;
+        if (g.t == 0) put_id(a, r, V - 1);
         if (orow) for_row(xrow, V, vec, g.t, X, [&](int i, float x) { orow[i] = x; });
         if (prow)
             for (int i = g.t; i < V; i += kTW) prow[i] = __builtin_nan("");
@@ -700,7 +700,7 @@ __device__ __forceinline__ void wide_general_row(const SampleArgs& a, int vec, i
                 for (int i = g.t; i < V; i += kTW) prow[i] = 0.0;
             __syncthreads();
             const int id = exact_block(g, s, n, mx, P.top_p < 1.0f, P.top_p, u, prow);
-            if (g.t == 0) a.out_ids[r] = id;
+            if (g.t == 0) put_id(a, r, id);
             return;
         }
     }
@@ -903,7 +903,7 @@ __device__ __forceinline__ void wide_general_row(const SampleArgs& a, int vec, i
         });
         pick = max((int)g.umax((uint32_t)(li + 1)) - 1, 0);
     }
-    if (g.t == 0) a.out_ids[r] = pick;
+    if (g.t == 0) put_id(a, r, pick);
     if (prow) {
         double se = 0.0;
         for_row(xrow, V, vec, g.t, X, [&](int i, float x) {
@@ -1178,7 +1178,7 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
     if (g.any(M != M || M * invT == kPosInf))
         for_row(xrow, V, vec, g.t, X, [&](int, float v) { bad |= __builtin_amdgcn_class(v, 0x203); });
     if (g.any(bad)) {
-        if (g.t == 0) a.out_ids[r] = VXS_ERR_NONFINITE;
+        if (g.t == 0) put_id(a, r, VXS_ERR_NONFINITE);
         return false;
     }
     // The finite count is the buffered total unless some wave compacted, which takes more than k
@@ -1198,7 +1198,7 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
     float* orow = a.out_logits ? a.out_logits + (int64_t)r * V : nullptr;
     double* prow = a.out_probs ? a.out_probs + (int64_t)r * V : nullptr;
     if (cnt == 0) {  // every entry -inf: the reference's draw returns the last id
-        if (g.t == 0) a.out_ids[r] = V - 1;
+        if (g.t == 0) put_id(a, r, V - 1);
         if (orow) for_row(xrow, V, vec, g.t, X, [&](int i, float x) { orow[i] = x; });
         if (prow)
             for (int i = g.t; i < V; i += kTW) prow[i] = __builtin_nan("");
@@ -1336,9 +1336,9 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
         for (int j = g.lane; j < n; j += 64) cp[j] = cp[j] / s2;
         wave_sync();
     }
-    const double u = a.u ? a.u[r] : 0.0;
+    const double u = row_uniform(a, r);
     const int pick = wave_draw(cp, s.ex.ci, n, u, scr, g.lane);  // inverse-CDF draw in index order :77-87
-    if (g.lane == 0) a.out_ids[r] = pick;
+    if (g.lane == 0) put_id(a, r, pick);
     if (prow)
         for (int j = g.lane; j < n; j += 64) prow[s.ex.ci[j]] = cp[j];
     return false;
