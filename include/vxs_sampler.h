@@ -132,6 +132,20 @@ VXS_API int vxs_sample_device(vxs_ctx* ctx, int rows, int vocab, const float* d_
                               uint32_t flags);
 
 /*
+ * vxs_sample for callers that cannot allocate (tight serving loops, harnesses that forbid hipMalloc):
+ * no counterpart in the reference. Same arguments, semantics and errors as vxs_sample without the
+ * write-back and probability outputs; synchronous. It allocates nothing: the inputs are copied from
+ * the caller's memory into a fixed 16 MiB device scratch (one per GPU, held until the process ends),
+ * the kernels read them there and write the ids there, and the ids are copied back. A call that
+ * needs more than the scratch (about rows * vocab * 4 bytes plus the histories, params and
+ * uniforms) fails with VXS_ERR_UNSUPPORTED. Every context on one GPU shares that GPU's scratch:
+ * calls that overlap on one GPU (from several threads or contexts) race; serialise them.
+ */
+VXS_API int vxs_sample_noalloc(vxs_ctx* ctx, int rows, int vocab, const float* logits, int64_t ld,
+                               const int32_t* hist_off, const int32_t* hist_ids, const vxs_params* params,
+                               int params_stride, const double* u, int32_t* out_ids, uint32_t flags);
+
+/*
  * Parity/debug variant of vxs_sample_device (no counterpart in the reference): no write-back or
  * probabilities; instead, for every row sampled by the one-wave nucleus regime (the wave path's
  * own work: sampled rows without top-k, vocab <= 3072),

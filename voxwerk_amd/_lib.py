@@ -90,6 +90,7 @@ _SIGNATURES = {
     "vxs_get_stream": (c_void_p, [c_void_p]),
     "vxs_sample": (c_int, [c_void_p, c_int, c_int, _P, c_int64, _P, _P, _P, c_int, _P, _P, _P, _P, c_uint32]),
     "vxs_sample_device": (c_int, [c_void_p, c_int, c_int, _P, c_int64, _P, _P, _P, c_int, _P, _P, _P, _P, c_uint32]),
+    "vxs_sample_noalloc": (c_int, [c_void_p, c_int, c_int, _P, c_int64, _P, _P, _P, c_int, _P, _P, c_uint32]),
     "vxs_sample_stats_device": (c_int, [c_void_p, c_int, c_int, _P, c_int64, _P, _P, _P, c_int, _P, _P, _P,
                                         c_uint32]),
     "vxs_synchronize": (c_int, [c_void_p]),

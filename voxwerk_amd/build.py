@@ -31,7 +31,8 @@ HIP_FLAGS = [
     "-Wall",
     f"-I{INCLUDE}",
 ]
-HIP_SOURCES = ["vxs_kernels.hip", "vxs_wide.hip", "vxs_history.hip", "vxs_embed.hip", "vxs_head.hip", "vxs_api.cpp"]
+HIP_SOURCES = ["vxs_kernels.hip", "vxs_wide.hip", "vxs_history.hip", "vxs_embed.hip", "vxs_head.hip", "vxs_noalloc.hip",
+               "vxs_api.cpp"]
 
 
 def _run(cmd: list[str], cwd: str = REPO) -> None:

@@ -92,6 +92,7 @@ struct vxs_ctx {
     bool done_ready = false;
     HostBuf h_done;
     uint32_t done_seq = 0;  // wraps; the completion word is reset to seq - 1 before each launch
+    void* noalloc = nullptr;  // this device's fixed scratch (vxs_sample_noalloc), looked up at create
 };
 
 struct vxs_history {
@@ -512,6 +513,11 @@ VXS_API int vxs_create(vxs_ctx** out, int device, int max_rows, int max_vocab, i
         return VXS_ERR_HIP;
     }
     ctx->stream = ctx->own_stream;
+    // the fixed scratch's device address on this device (the device is current)
+    if (vxs::noalloc_scratch(device, &ctx->noalloc) != hipSuccess) {
+        vxs_destroy(ctx);
+        return VXS_ERR_HIP;
+    }
     if (max_rows > 0 && max_vocab > 0) {
         const int32_t* no_hist = nullptr;
         Layout L = plan(max_rows, max_vocab, 1, no_hist);
@@ -602,6 +608,78 @@ VXS_API int vxs_sample(vxs_ctx* ctx, int rows, int vocab, const float* logits, i
         return first_row_error(ctx, out_ids, rows);
     } catch (const std::exception& e) {
         return fail(ctx, VXS_ERR_INVALID_ARG, e.what());
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
+VXS_API int vxs_sample_noalloc(vxs_ctx* ctx, int rows, int vocab, const float* logits, int64_t ld,
+                               const int32_t* hist_off, const int32_t* hist_ids, const vxs_params* params,
+                               int params_stride, const double* u, int32_t* out_ids, uint32_t flags) {
+    try {
+        int rc = check_shape(ctx, rows, vocab, logits, ld, params, params_stride, out_ids);
+        if (rc != VXS_OK) return rc;
+        if ((rc = check_flags(ctx, flags)) != VXS_OK) return rc;
+        if (rows == 0) return VXS_OK;
+        if ((rc = check_params_host(ctx, rows, params, params_stride, u)) != VXS_OK) return rc;
+        if ((rc = check_hist_host(ctx, rows, hist_off, hist_ids)) != VXS_OK) return rc;
+        if (!ctx->noalloc) return fail(ctx, VXS_ERR_HIP, "no fixed scratch on this device");
+        // the staged layout of vxs_sample, then the ids, all inside the fixed scratch
+        const Layout L = plan(rows, vocab, params_stride, hist_off);
+        const size_t ids_at = L.total;
+        const size_t need = align_up(ids_at + sizeof(int32_t) * (size_t)rows);
+        if (need > vxs::kNoAllocScratchBytes)
+            return fail(ctx, VXS_ERR_UNSUPPORTED,
+                        "vxs_sample_noalloc: this call stages " + std::to_string(need) + " bytes; the fixed scratch holds " +
+                            std::to_string(vxs::kNoAllocScratchBytes));
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        char* d = static_cast<char*>(ctx->noalloc);
+        hipStream_t st = ctx->stream;
+        // inputs straight from the caller's memory (no pinned staging)
+        if (params_stride <= 1) {
+            VXS_HIP(ctx, hipMemcpyAsync(d + L.params, params, sizeof(vxs_params) * (size_t)L.np, hipMemcpyHostToDevice, st));
+        } else {
+            VXS_HIP(ctx, hipMemcpy2DAsync(d + L.params, sizeof(vxs_params), params, sizeof(vxs_params) * (size_t)params_stride,
+                                          sizeof(vxs_params), (size_t)rows, hipMemcpyHostToDevice, st));
+        }
+        if (u) VXS_HIP(ctx, hipMemcpyAsync(d + L.u, u, sizeof(double) * (size_t)rows, hipMemcpyHostToDevice, st));
+        const int32_t* k_hoff = nullptr;
+        const int32_t* k_hids = nullptr;
+        if (hist_off) {
+            // the offsets as given; the ids from hist_off[0] on, so the kernel's base is shifted back
+            VXS_HIP(ctx, hipMemcpyAsync(d + L.hoff, hist_off, sizeof(int32_t) * (size_t)(rows + 1), hipMemcpyHostToDevice, st));
+            if (L.nh)
+                VXS_HIP(ctx, hipMemcpyAsync(d + L.hids, hist_ids + hist_off[0], sizeof(int32_t) * (size_t)L.nh,
+                                            hipMemcpyHostToDevice, st));
+            k_hoff = reinterpret_cast<const int32_t*>(d + L.hoff);
+            k_hids = reinterpret_cast<const int32_t*>(reinterpret_cast<uintptr_t>(d + L.hids) -
+                                                      sizeof(int32_t) * (uintptr_t)(int64_t)hist_off[0]);
+        }
+        if (ld == L.ld_dev) {
+            VXS_HIP(ctx, hipMemcpyAsync(d + L.logits, logits, sizeof(float) * ((size_t)(rows - 1) * (size_t)ld + (size_t)vocab),
+                                        hipMemcpyHostToDevice, st));
+        } else {
+            VXS_HIP(ctx, hipMemcpy2DAsync(d + L.logits, sizeof(float) * (size_t)L.ld_dev, logits, sizeof(float) * (size_t)ld,
+                                          sizeof(float) * (size_t)vocab, (size_t)rows, hipMemcpyHostToDevice, st));
+        }
+        vxs::SampleArgs a{};
+        a.rows = rows;
+        a.vocab = vocab;
+        a.ld = L.ld_dev;
+        a.logits = reinterpret_cast<const float*>(d + L.logits);
+        a.hist_off = k_hoff;
+        a.hist_ids = k_hids;
+        a.params = reinterpret_cast<const vxs_params*>(d + L.params);
+        a.params_stride = params_stride == 0 ? 0 : 1;
+        a.u = u ? reinterpret_cast<const double*>(d + L.u) : nullptr;
+        a.out_ids = reinterpret_cast<int32_t*>(d + ids_at);
+        a.kflags = 0;
+        a.path = choose_path_host(flags, rows, vocab, params, params_stride);
+        VXS_HIP(ctx, vxs::launch_sample(a, st));
+        VXS_HIP(ctx, hipMemcpyAsync(out_ids, d + ids_at, sizeof(int32_t) * (size_t)rows, hipMemcpyDeviceToHost, st));
+        VXS_HIP(ctx, hipStreamSynchronize(st));
+        ctx->err.clear();
+        return first_row_error(ctx, out_ids, rows);
     } catch (...) {
         return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
     }

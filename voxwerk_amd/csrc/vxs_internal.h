@@ -212,6 +212,11 @@ struct HeadArgs {
 hipError_t launch_head(const HeadArgs& a, hipStream_t stream);
 hipError_t launch_frame_embed(const FrameEmbedArgs& a, hipStream_t stream);
 
+// Fixed device scratch of vxs_sample_noalloc (vxs_noalloc.hip): its size, and its device address on
+// `device`, which must be the current device (looked up once per device, then cached).
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+hipError_t noalloc_scratch(int device, void** out);
+
 // Enqueue the sampler on `stream`. Returns hipSuccess or the launch error.
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream);
 hipError_t launch_sample_wide(const SampleArgs& a, hipStream_t stream);
