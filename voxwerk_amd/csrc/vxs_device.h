@@ -445,6 +445,79 @@ __device__ __forceinline__ int wave_draw(const double* p, const int32_t* id, int
     return last >= 0 ? id[last] : 0;
 }
 
+// LDS ordering inside one wave.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The reference's sequential fp64 arithmetic (Sampler.cs:51-87) on n <= 64 candidates by one wave,
+// candidate j (index order) in lane j: x = its logit after temperature and the top-k mask, m = the
+// row maximum; ids[0..n) their vocabulary indices (LDS). Entries outside the candidates have p = 0:
+// they add nothing to any sum, sort first in the top-p order (where the loop passes over them) and
+// are never drawn. The sequential sums read their terms from LDS in batches (the reads of a batch
+// issued before its adds), every lane adding the same terms in the reference's order; ranks and the
+// crossings are lane-parallel. scr: 256 doubles of wave-private LDS. Returns the sampled id
+// (uniform); with prow, lanes < n store their final probability to prow[ids[lane]].
+__device__ __forceinline__ int wave_exact(float x, const int32_t* ids, int n, float m, bool topp, float top_p,
+                                          double u, double* scr, double* prow, int lane) {
+    n = __builtin_amdgcn_readfirstlane(n);  // uniform in fact; so the compiler keeps the loops scalar
+    double* cp = scr;                                    // p in index order
+    double* ps = scr + 64;                               // p in (p, index) order
+    uint64_t* key = reinterpret_cast<uint64_t*>(scr + 128);  // sort keys, then lanes by sorted position
+    double* pre = scr + 192;                             // running sums of the cut and the draw
+    const bool in = lane < n;
+    double p = in ? exp((double)(x - m)) : 0.0;  // :57, x - m in fp32, then Math.Exp
+    cp[lane] = p;
+    wave_lds_sync();
+    p = in ? p / seq_sum(cp, n) : 0.0;  // :58-60, the sum in index order
+    if (topp) {  // :62-75
+        // Stable ascending (p, index) order. p = exp(d) / sum never decreases with d = fl32(x - m),
+        // so the (d, index) order is taken when every adjacent pair of it is in (p, index) order,
+        // else the entries are ranked by p directly.
+        const uint64_t k = in ? ((uint64_t)f2key(x - m) << 32) | (uint32_t)lane : ~0ull;
+        key[lane] = k;
+        cp[lane] = p;
+        wave_lds_sync();
+        int rank = 0;
+#pragma unroll 8
+        for (int l = 0; l < n; l++) rank += key[l] < k ? 1 : 0;
+        wave_lds_sync();  // every lane has read the keys
+        int* at = reinterpret_cast<int*>(key);
+        if (in) {
+            ps[rank] = p;
+            at[rank] = lane;
+        }
+        wave_lds_sync();
+        const bool has_next = in && rank + 1 < n;
+        const double pn = ps[has_next ? rank + 1 : 0];
+        const int ln = at[has_next ? rank + 1 : 0];
+        if (__ballot(has_next && !(p < pn || (p == pn && lane < ln)))) {
+            rank = 0;
+#pragma unroll 8
+            for (int l = 0; l < n; l++) {
+                const double pl = cp[l];
+                rank += (pl < p || (pl == p && l < lane)) ? 1 : 0;
+            }
+            wave_lds_sync();  // every lane has read ps above
+            if (in) ps[rank] = p;
+            wave_lds_sync();
+        }
+        // positions 0 .. n - 2 are removed while the running sum stays <= 1 - top_p
+        const int nrem = wave_topp_cut(ps, n, (double)(1.0f - top_p), pre, lane);
+        if (in && rank < nrem) p = 0.0;
+        wave_lds_sync();  // the cut has read ps and pre
+        cp[lane] = p;
+        wave_lds_sync();
+        p = in ? p / seq_sum(cp, n) : 0.0;  // probs.Sum() in index order, then :74
+    }
+    if (prow && in) prow[ids[lane]] = p;
+    cp[lane] = p;
+    wave_lds_sync();
+    return wave_draw(cp, ids, n, u, pre, lane);  // :77-87
+}
+
 // Stable ascending (p, index) rank of entry j among p[0..n).
 __device__ __forceinline__ int seq_rank(const double* p, int n, int j) {
     const double pj = p[j];

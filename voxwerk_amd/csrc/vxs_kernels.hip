@@ -207,7 +207,7 @@ struct RowSmem {
         } sel;
         double nh[NC][C::NBP];  // nucleus histograms, one per sweep
         struct {
-            float cx[kCandMax];
+            alignas(16) float cx[kCandMax];
             int32_t ci[kCandMax];
             double cp[kCandMax];
             double ps[kCandMax];   // p in (p, index) order, for the top-p cut
@@ -542,7 +542,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
     HistRange hr{0, 0};
     if (has_history(a)) hr = history_range(a, r);
     const bool pen_on = P.rep_penalty != 1.0f && has_history(a);
-    constexpr int HP = 2;  // ids per thread fetched up front (512 per row)
+    constexpr int HP = 8;  // ids per thread fetched up front (2048 per row), in flight with the row
     const int h0 = hr.h0, h1 = pen_on ? hr.h1 : hr.h0;
     int pre[HP];
     if (pen_on) {
@@ -577,9 +577,27 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
             const uint32_t bit = 1u << (id & 31);
             if (!(atomicOr(&sm.bm[id >> 5], bit) & bit)) xs[id] = penalize(xs[id], rho, rinv, fast);
         };
+        {
+            // the prefetched ids: every bitmap atomic issued before any owner rescales its logit
+            // (an id's owner is unique, so the rescales touch distinct entries)
+            uint32_t won = 0;
 #pragma unroll
-        for (int k = 0; k < HP; k++)
-            if (h0 + g.t + k * kT < h1) own(pre[k]);
+            for (int k = 0; k < HP; k++) {
+                const int id = pre[k];
+                const bool in = h0 + g.t + k * kT < h1;
+                if (in && (unsigned)id >= (unsigned)V) bad = true;
+                if (in && (unsigned)id < (unsigned)V) {
+                    const uint32_t bit = 1u << (id & 31);
+                    won |= (atomicOr(&sm.bm[id >> 5], bit) & bit) ? 0u : 1u << k;
+                }
+            }
+            float xv[HP];
+#pragma unroll
+            for (int k = 0; k < HP; k++) xv[k] = (won >> k) & 1u ? xs[pre[k]] : 0.0f;
+#pragma unroll
+            for (int k = 0; k < HP; k++)
+                if ((won >> k) & 1u) xs[pre[k]] = penalize(xv[k], rho, rinv, fast);
+        }
         for (int hb = h0 + HP * kT; hb < h1; hb += 4 * kT) {  // the rest, four ids per thread in flight
             int id[4];
 #pragma unroll
@@ -800,8 +818,15 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
             if (g.t < n) {
                 const float x = ex.cx[g.t];
                 int gt = 0, ge = 0;
-#pragma unroll 8
-                for (int l = 0; l < n; l++) {
+                typedef float f4v __attribute__((ext_vector_type(4)));
+                const int n4 = n & ~3;
+#pragma unroll 4
+                for (int l = 0; l < n4; l += 4) {
+                    const f4v y = *reinterpret_cast<const f4v*>(&ex.cx[l]);
+                    gt += (y.x > x ? 1 : 0) + (y.y > x ? 1 : 0) + (y.z > x ? 1 : 0) + (y.w > x ? 1 : 0);
+                    ge += (y.x >= x ? 1 : 0) + (y.y >= x ? 1 : 0) + (y.z >= x ? 1 : 0) + (y.w >= x ? 1 : 0);
+                }
+                for (int l = n4; l < n; l++) {
                     const float y = ex.cx[l];
                     gt += y > x ? 1 : 0;
                     ge += y >= x ? 1 : 0;
@@ -930,9 +955,38 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
             for (int e = 0; e < NE; e++)
                 if (eidx(e) < V && v[e] == kNegInf) prow[eidx(e)] = 0.0;
         g.sync();
+        const int n = cands ? ncand : (int)cnt;
+        if (cnt <= 64u) {
+            // One wave takes the row; the other waves are done with it. The live candidates (the
+            // top-k path also gathers entries below the k-th value, masked to -inf) are compacted
+            // in index order into ex.cp's storage, one per lane.
+            if (g.wv == 0) {
+                float* cx = reinterpret_cast<float*>(ex.cp);
+                int32_t* ci = reinterpret_cast<int32_t*>(ex.cp + 32);
+                uint32_t base = 0;
+                for (int q = 0; q < n; q += 64) {  // n uniform (a count every thread computed)
+                    const int j = q + g.lane;
+                    const float xj = j < n ? ex.cx[j] : kNegInf;
+                    const bool live = xj != kNegInf;
+                    const uint64_t bal = __ballot(live);
+                    const uint32_t at = base + (uint32_t)__builtin_amdgcn_mbcnt_hi(
+                                                   (uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+                    if (live) {
+                        cx[at] = xj;
+                        ci[at] = ex.ci[j];
+                    }
+                    base += (uint32_t)__builtin_popcountll(bal);
+                }
+                wave_lds_sync();
+                const int nl = (int)cnt;
+                const float xl = g.lane < nl ? cx[g.lane] : 0.0f;
+                const int pick = wave_exact(xl, ci, nl, m, topp, P.top_p, u, ex.ps, prow, g.lane);
+                if (g.lane == 0) put_id(a, r, pick);
+            }
+            return;
+        }
         // Parallel phases stride the candidates over the workgroup; sequential phases run
         // redundantly in every thread on LDS broadcast reads, so each yields a uniform value.
-        const int n = cands ? ncand : (int)cnt;
         for (int j = g.t; j < n; j += kT) ex.cp[j] = exp((double)(ex.cx[j] - m));  // Sampler.cs:57
         g.sync();
         double sum = seq_sum(ex.cp, n);  // sequential in index order                      :58
