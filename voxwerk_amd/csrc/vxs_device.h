@@ -332,116 +332,77 @@ __device__ __forceinline__ int seq_draw(const double* p, const int32_t* id, int 
     return lastj >= 0 ? id[lastj] : 0;
 }
 
-// ---- one-wave forms of the top-p cut and the draw: the dependent loop only adds and records
-// each prefix (lane 0 stores it to LDS scratch, 8 at a time); the compares then run lane-parallel
-// over the recorded prefixes. Same results as seq_topp_cut and seq_draw.
+// ---- one-wave forms of the top-p cut and the draw: every lane runs the same dependent chain of
+// additions over LDS reads in batches of eight (the reads of a batch issued before its adds); the
+// running sum never decreases until it turns NaN, so the batch that holds the deciding prefix is
+// the first whose last prefix decides, and the prefix is found among that batch's eight. Same
+// results as seq_topp_cut and seq_draw.
 
 // seq_topp_cut by one wave, on the probabilities already gathered into sorted order
-// (ps[s] = p[order[s]]); scr holds n - 1 doubles of LDS. The next batch of eight is read while
-// the current one is added.
-__device__ __forceinline__ int wave_topp_cut(const double* ps, int n, double thr, double* scr, int lane) {
+// (ps[s] = p[order[s]]): the number of leading positions, among the first n - 1, whose running sum
+// stays <= thr.
+__device__ __forceinline__ int wave_topp_cut(const double* ps, int n, double thr) {
     const int m = n - 1;  // the positions the reference may remove
     double cum = 0.0;
-    int end = 0;  // prefixes recorded
-    bool over = false;
-    if (m >= 8) {
-        double nx[8];
+    int j = 0;
+    for (; j + 8 <= m; j += 8) {
+        double b[8], c[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) nx[k] = ps[k];
-        while (true) {
-            double cur[8];
+        for (int k = 0; k < 8; k++) b[k] = ps[j + k];
 #pragma unroll
-            for (int k = 0; k < 8; k++) cur[k] = nx[k];
-            const int nb = end + 8;
-            if (nb + 8 <= m)
+        for (int k = 0; k < 8; k++) {
+            cum += b[k];
+            c[k] = cum;
+        }
+        if (!(cum <= thr)) {
+            int f = 8;
 #pragma unroll
-                for (int k = 0; k < 8; k++) nx[k] = ps[nb + k];
-            double c[8];
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                cum += cur[k];
-                c[k] = cum;
-            }
-            if (lane == 0)
-#pragma unroll
-                for (int k = 0; k < 8; k++) scr[end + k] = c[k];
-            end = nb;
-            // the deciding prefix is recorded: the rest exceed thr (or are NaN)
-            over = __builtin_amdgcn_readfirstlane(!(cum <= thr) ? 1 : 0) != 0;
-            if (over || end + 8 > m) break;
+            for (int k = 7; k >= 0; k--) f = !(c[k] <= thr) ? k : f;
+            return j + f;
         }
     }
-    for (; end < m && !over; end++) {
-        cum += ps[end];
-        if (lane == 0) scr[end] = cum;
-        over = __builtin_amdgcn_readfirstlane(!(cum <= thr) ? 1 : 0) != 0;
+    for (; j < m; j++) {
+        cum += ps[j];
+        if (!(cum <= thr)) return j;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    uint32_t cnt = 0;
-    for (int q = lane; q < end; q += 64) cnt += scr[q] <= thr ? 1u : 0u;
-    return (int)wave_sum(cnt);
+    return m;
 }
 
-// seq_draw by one wave; scr holds n doubles of LDS. Skipped entries (p <= 0) hold +0 here (the
-// probabilities are exp(d) / sum >= +0, removed ones +0), so adding them leaves the running sum
-// unchanged and the loop adds every entry. The next batch of eight is read while the current one
-// is added.
-__device__ __forceinline__ int wave_draw(const double* p, const int32_t* id, int n, double u, double* scr,
-                                         int lane) {
+// seq_draw by one wave over p[0..n) with ids id[0..n): the first entry whose running sum exceeds u,
+// or without one the last entry with p > 0 or NaN (0 when none). Skipped entries (p <= 0) hold +0
+// here (the probabilities are exp(d) / sum >= +0, removed ones +0), so adding them leaves the
+// running sum unchanged and the chain adds every entry.
+__device__ __forceinline__ int wave_draw(const double* p, const int32_t* id, int n, double u) {
     double acc = 0.0;
-    int end = 0;
-    bool stop = false;  // a prefix above u (or NaN) is recorded
-    if (n >= 8) {
-        double nx[8];
+    int j = 0, pick = -1;
+    for (; j + 8 <= n; j += 8) {
+        double b[8], c[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) nx[k] = p[k];
-        while (true) {
-            double cur[8];
+        for (int k = 0; k < 8; k++) b[k] = p[j + k];
 #pragma unroll
-            for (int k = 0; k < 8; k++) cur[k] = nx[k];
-            const int nb = end + 8;
-            if (nb + 8 <= n)
+        for (int k = 0; k < 8; k++) {
+            acc += b[k];
+            c[k] = acc;
+        }
+        if (!(acc <= u)) {  // the crossing, or a NaN prefix, is in this batch
+            int f = 8;
 #pragma unroll
-                for (int k = 0; k < 8; k++) nx[k] = p[nb + k];
-            double c[8];
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                acc += cur[k];
-                c[k] = acc;
-            }
-            if (lane == 0)
-#pragma unroll
-                for (int k = 0; k < 8; k++) scr[end + k] = c[k];
-            end = nb;
-            stop = __builtin_amdgcn_readfirstlane(!(acc <= u) ? 1 : 0) != 0;
-            if (stop || end + 8 > n) break;
+            for (int k = 7; k >= 0; k--) f = !(c[k] <= u) ? k : f;
+            if (u < c[f]) pick = j + f;  // a NaN prefix first: no crossing at all
+            break;
         }
     }
-    for (; end < n && !stop; end++) {
-        acc += p[end];
-        if (lane == 0) scr[end] = acc;
-        stop = __builtin_amdgcn_readfirstlane(!(acc <= u) ? 1 : 0) != 0;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // the running sum never decreases until it turns NaN: the first crossing is the number of
-    // prefixes <= u, provided that is below the first NaN prefix
-    uint32_t below = 0, first_nan = (uint32_t)n;
-    for (int q = lane; q < end; q += 64) {
-        const double a = scr[q];
-        below += a <= u ? 1u : 0u;
-        if (a != a) first_nan = min(first_nan, (uint32_t)q);
-    }
-    below = wave_sum(below);
-    first_nan = wave_umin(first_nan);
-    if (below < first_nan) return id[below];
-    // no crossing: the last entry with p > 0 or NaN (0 when none)
+    if (pick < 0 && acc <= u)
+        for (; j < n; j++) {
+            acc += p[j];
+            if (!(acc <= u)) {
+                if (u < acc) pick = j;
+                break;
+            }
+        }
+    if (pick >= 0) return id[pick];
     int last = -1;
-    for (int q = lane; q < n; q += 64) last = !(p[q] <= 0.0) ? q : last;
-    last = (int)wave_umax((uint32_t)(last + 1)) - 1;
+    for (int q = 0; q < n; q++) last = !(p[q] <= 0.0) ? q : last;
     return last >= 0 ? id[last] : 0;
 }
 
@@ -458,15 +419,14 @@ __device__ __forceinline__ void wave_lds_sync() {
 // they add nothing to any sum, sort first in the top-p order (where the loop passes over them) and
 // are never drawn. The sequential sums read their terms from LDS in batches (the reads of a batch
 // issued before its adds), every lane adding the same terms in the reference's order; ranks and the
-// crossings are lane-parallel. scr: 256 doubles of wave-private LDS. Returns the sampled id
+// crossings are found in register batches. scr: 192 doubles of wave-private LDS. Returns the sampled id
 // (uniform); with prow, lanes < n store their final probability to prow[ids[lane]].
 __device__ __forceinline__ int wave_exact(float x, const int32_t* ids, int n, float m, bool topp, float top_p,
                                           double u, double* scr, double* prow, int lane) {
     n = __builtin_amdgcn_readfirstlane(n);  // uniform in fact; so the compiler keeps the loops scalar
-    double* cp = scr;                                    // p in index order
-    double* ps = scr + 64;                               // p in (p, index) order
+    double* cp = scr;                                        // p in index order
+    double* ps = scr + 64;                                   // p in (p, index) order
     uint64_t* key = reinterpret_cast<uint64_t*>(scr + 128);  // sort keys, then lanes by sorted position
-    double* pre = scr + 192;                             // running sums of the cut and the draw
     const bool in = lane < n;
     double p = in ? exp((double)(x - m)) : 0.0;  // :57, x - m in fp32, then Math.Exp
     cp[lane] = p;
@@ -505,9 +465,9 @@ __device__ __forceinline__ int wave_exact(float x, const int32_t* ids, int n, fl
             wave_lds_sync();
         }
         // positions 0 .. n - 2 are removed while the running sum stays <= 1 - top_p
-        const int nrem = wave_topp_cut(ps, n, (double)(1.0f - top_p), pre, lane);
+        const int nrem = wave_topp_cut(ps, n, (double)(1.0f - top_p));
         if (in && rank < nrem) p = 0.0;
-        wave_lds_sync();  // the cut has read ps and pre
+        wave_lds_sync();  // the cut has read ps
         cp[lane] = p;
         wave_lds_sync();
         p = in ? p / seq_sum(cp, n) : 0.0;  // probs.Sum() in index order, then :74
@@ -515,7 +475,7 @@ __device__ __forceinline__ int wave_exact(float x, const int32_t* ids, int n, fl
     if (prow && in) prow[ids[lane]] = p;
     cp[lane] = p;
     wave_lds_sync();
-    return wave_draw(cp, ids, n, u, pre, lane);  // :77-87
+    return wave_draw(cp, ids, n, u);  // :77-87
 }
 
 // Stable ascending (p, index) rank of entry j among p[0..n).

@@ -1028,7 +1028,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
             for (int q = g.t; q < n; q += kT) ex.ps[q] = ex.cp[ex.cs[q]];
             g.sync();
             if (g.wv == 0) {
-                const int nr = wave_topp_cut(ex.ps, n, thr, ex.pre, g.lane);
+                const int nr = wave_topp_cut(ex.ps, n, thr);
                 if (g.lane == 0) ex.nrem = nr;
             }
             g.sync();
@@ -1041,7 +1041,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
             g.sync();
         }
         if (g.wv == 0) {  // inverse-CDF draw in index order                              :77-87
-            const int pick = wave_draw(ex.cp, ex.ci, n, u, ex.pre, g.lane);
+            const int pick = wave_draw(ex.cp, ex.ci, n, u);
             if (g.lane == 0) put_id(a, r, pick);
         }
         if (prow)

@@ -1279,11 +1279,15 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
         const uint64_t kt = ckey[g.t];
         cxt = s.ex.cx[g.t];
         cit = s.ex.ci[g.t];
-#pragma unroll 8
-        for (int l = 0; l < n; l++) {
-            const uint64_t kl = ckey[l];
-            io += (uint32_t)kl < (uint32_t)kt ? 1 : 0;
-            po += kl < kt ? 1 : 0;
+        // two keys per LDS read; a pair past n reads a stale slot, not counted
+        typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
+#pragma unroll 4
+        for (int l = 0; l < n; l += 2) {
+            const u64x2 kl = *reinterpret_cast<const u64x2*>(&ckey[l]);
+            io += (uint32_t)kl.x < (uint32_t)kt ? 1 : 0;
+            po += kl.x < kt ? 1 : 0;
+            io += (l + 1 < n && (uint32_t)kl.y < (uint32_t)kt) ? 1 : 0;
+            po += (l + 1 < n && kl.y < kt) ? 1 : 0;
         }
     }
     __syncthreads();
@@ -1297,7 +1301,6 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
 
     // ---- the worker wave: the reference's fp64 arithmetic on the candidates in index order
     double* cp = s.ex.cp;
-    double* scr = reinterpret_cast<double*>(&s.wkey[0][0]);  // the prefixes of the cut and the draw
     for (int j = g.lane; j < n; j += 64) cp[j] = exp((double)(s.ex.cx[j] - mx));  // Sampler.cs:57
     wave_sync();
     const double sum = seq_sum(cp, n);  // sequential in index order                   :58
@@ -1329,7 +1332,7 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
         double* ps = reinterpret_cast<double*>(&s.widx[0][0]);  // p in (p, index) order
         for (int q = g.lane; q < n; q += 64) ps[q] = cp[s.ex.cs[q]];
         wave_sync();
-        const int nrem = wave_topp_cut(ps, n, (double)(1.0f - P.top_p), scr, g.lane);
+        const int nrem = wave_topp_cut(ps, n, (double)(1.0f - P.top_p));
         for (int q = g.lane; q < nrem; q += 64) cp[s.ex.cs[q]] = 0.0;
         wave_sync();
         const double s2 = seq_sum(cp, n);
@@ -1337,7 +1340,7 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
         wave_sync();
     }
     const double u = row_uniform(a, r);
-    const int pick = wave_draw(cp, s.ex.ci, n, u, scr, g.lane);  // inverse-CDF draw in index order :77-87
+    const int pick = wave_draw(cp, s.ex.ci, n, u);  // inverse-CDF draw in index order :77-87
     if (g.lane == 0) put_id(a, r, pick);
     if (prow)
         for (int j = g.lane; j < n; j += 64) prow[s.ex.ci[j]] = cp[j];
