@@ -270,6 +270,57 @@ __device__ __forceinline__ double seq_sum(const double* x, int n) {
     return s;
 }
 
+// seq_sum with the next batch of eight read while the current one is added (x 16-byte aligned): for
+// long sums, where the read latency of each batch would otherwise add to the chain.
+__device__ __forceinline__ double seq_sum_pipe(const double* x, int n) {
+    typedef double d2 __attribute__((ext_vector_type(2)));
+    const d2* v = reinterpret_cast<const d2*>(x);
+    double s = 0.0;
+    int j = 0;
+    if (n >= 8) {
+        // b holds the batch before j, read but not yet added
+        d2 b[4], c[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) b[k] = v[k];
+        j = 8;
+        for (; j + 16 <= n; j += 16) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) c[k] = v[j / 2 + k];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                s += b[k].x;
+                s += b[k].y;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) b[k] = v[j / 2 + 4 + k];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                s += c[k].x;
+                s += c[k].y;
+            }
+        }
+        if (j + 8 <= n) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) c[k] = v[j / 2 + k];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                s += b[k].x;
+                s += b[k].y;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) b[k] = c[k];
+            j += 8;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            s += b[k].x;
+            s += b[k].y;
+        }
+    }
+    for (; j < n; j++) s += x[j];
+    return s;
+}
+
 // Top-p cut over the (p, index)-sorted order (order[s] = entry at sorted position s): the number
 // of leading positions, among the first n - 1, whose running sum stays <= thr (Sampler.cs:66-73).
 // The running sum never decreases until it turns NaN (and stays NaN), so the reference's first
@@ -366,6 +417,52 @@ __device__ __forceinline__ int wave_topp_cut(const double* ps, int n, double thr
         if (!(cum <= thr)) return j;
     }
     return m;
+}
+
+// wave_topp_cut for n <= 256 without the dependent chain, same result. Lane l sums positions
+// 4l..4l+3 and a wave scan adds the lanes before it: every prefix sum P_j of the first n - 1
+// probabilities with at most 10 roundings on any term's path, so |P_j - T_j| <= 10 u T_j for the
+// exact prefix sum T_j (u = 2^-53, the terms are non-negative). The reference's running sum C_j,
+// j + 1 <= 255 terms added left to right, has |C_j - T_j| <= 254 u T_j (Higham, Accuracy and
+// Stability of Numerical Algorithms, 2nd ed., 4.2), so |C_j - P_j| < 2^-44 P_j. C_j never decreases,
+// so the first j with C_j > thr is the first j with P_j > thr whenever P_j (1 - 2^-40) > thr and
+// P_{j-1} (1 + 2^-40) <= thr (no crossing: P_{m-1} (1 + 2^-40) <= thr). With thr that close to a
+// prefix sum, or NaN, the sequential form decides.
+__device__ __forceinline__ int wave_topp_cut_par(const double* ps, int n, double thr, int lane) {
+    const int m = n - 1;  // the positions the reference may remove
+    if (n > 256) return wave_topp_cut(ps, n, thr);
+    if (m <= 0) return 0;
+    const int j0 = 4 * lane;
+    double P[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) P[k] = j0 + k < m ? ps[j0 + k] : 0.0;
+    P[1] += P[0];
+    P[2] += P[1];
+    P[3] += P[2];
+    const double incl = wave_incl_sum(P[3]);
+    double excl = __shfl_up(incl, 1);
+    excl = lane == 0 ? 0.0 : excl;
+#pragma unroll
+    for (int k = 0; k < 4; k++) P[k] += excl;
+    int f = 4;  // this lane's first position with P_j > thr (or NaN)
+#pragma unroll
+    for (int k = 3; k >= 0; k--) f = (j0 + k < m && !(P[k] <= thr)) ? k : f;
+    const uint64_t bal = __ballot(f < 4);
+    constexpr double kUp = 1.0 + 0x1p-40, kDown = 1.0 - 0x1p-40;
+    if (bal == 0) {  // no P_j above thr: C_j stays <= thr for every j < m if P_{m-1} is clear of it
+        const int lm = (m - 1) >> 2, km = (m - 1) & 3;
+        const double pl = km == 0 ? P[0] : km == 1 ? P[1] : km == 2 ? P[2] : P[3];
+        const double last = readlane_d(pl, lm);
+        if (last * kUp <= thr) return m;
+        return wave_topp_cut(ps, n, thr);
+    }
+    const int src = __builtin_ctzll(bal);
+    const double pf = f == 0 ? P[0] : f == 1 ? P[1] : f == 2 ? P[2] : P[3];
+    const double pb = f == 0 ? excl : f == 1 ? P[0] : f == 2 ? P[1] : P[2];  // the prefix before it
+    const int js = 4 * src + __builtin_amdgcn_readlane(f, src);
+    const double pj = readlane_d(pf, src), pp = readlane_d(pb, src);
+    if (pj * kDown > thr && (js == 0 || pp * kUp <= thr)) return js;
+    return wave_topp_cut(ps, n, thr);
 }
 
 // seq_draw by one wave over p[0..n) with ids id[0..n): the first entry whose running sum exceeds u,

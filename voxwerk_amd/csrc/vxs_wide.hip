@@ -41,14 +41,13 @@ constexpr int kCapW = 512;        // candidate buffer entries per wave
 constexpr int kPerL = kCapW / 64;  // ... per lane
 constexpr int kKMax = 256;        // largest top-k of the streaming path
 constexpr int kCandW = 256;       // exact-regime capacity
-constexpr int kUnion = 1536;      // ordered pass: the four buffers' entries after pass A, at most
 constexpr int kRB = 256;          // radix buckets (8-bit digits)
 // zero words after the history bitmap: a sweep's lanes past the row end (up to 255 entries) read
 // bitmap words within the allocation
 constexpr int kBmPad = 8;
 
 struct WideSmem {
-    uint32_t wkey[kWW][kCapW];  // per-wave candidate keys (f2key of the value)
+    alignas(16) uint32_t wkey[kWW][kCapW];  // per-wave candidate keys (f2key of the value)
     int32_t widx[kWW][kCapW];   // per-wave candidate indices
     // The radix histograms are done with before the exact-regime arrays are filled, so the two
     // share their storage: with the history bitmap of a 151936-entry row this keeps a workgroup
@@ -57,6 +56,7 @@ struct WideSmem {
         union {
             alignas(16) uint32_t hcnt[kRB];
             double hmass[kRB];
+            alignas(16) uint32_t h3[3 * kRB];  // ordered pass: the k-th largest select's histograms
         } h;
         struct {
             float cx[kCandW];
@@ -69,9 +69,11 @@ struct WideSmem {
     int32_t wcnt[kWW];  // per-wave candidate counts after pass A (-1: the wave's buffer overflowed)
     int32_t wcomp[kWW]; // per-wave: the buffer was compacted at least once (ordered pass)
     int32_t wslot[kWW]; // per-wave: the wave's SIMD matches the workgroup's slot on its CU (ordered pass)
+    uint32_t wklo[kWW], wkhi[kWW];  // ordered pass, per wave: smallest and largest buffered key ...
+    int32_t wbad[kWW];              // ... a NaN or fl(x * 1/T) = +inf in its range ...
+    int32_t wcand[kWW];             // ... and its candidates at or above the k-th largest
     uint32_t tau_key;   // the largest k-th largest any wave has found so far (a shared lower bound)
-    uint32_t kth_key;   // ordered pass: the row's k-th largest (0 without top-k) ...
-    float mx;           // ... and its maximum
+    uint32_t qkey[kWW]; // ordered pass, per wave: a key with at least ceil(k/4) of the wave's entries at or above it
     int32_t n;          // exact-regime candidates
 };
 
@@ -204,6 +206,32 @@ __device__ __forceinline__ uint32_t wave_kth_regs(const uint32_t (&kk)[N], uint3
     return lo;
 }
 
+// The digit of the need-th largest counted key, from a 256-bin histogram of the current digit read
+// by one wave (lane l takes bins 255 - 4l down to 252 - 4l, the counts in descending digit order);
+// need drops by the count of keys in higher digits.
+__device__ __forceinline__ uint32_t hist_digit(const uint32_t* hist, int lane, int& need) {
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    const u4 h4 = reinterpret_cast<const u4*>(hist)[63 - lane];
+    const uint32_t c[4] = {h4.w, h4.z, h4.y, h4.x};
+    const uint32_t tot = c[0] + c[1] + c[2] + c[3];
+    const uint32_t incl = wave_incl_sum(tot);
+    uint32_t run = incl - tot;  // entries in higher digits than this lane's
+    int digit = -1;
+    uint32_t above = 0;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        if (digit < 0 && run < (uint32_t)need && run + c[b] >= (uint32_t)need) {
+            digit = 255 - 4 * lane - b;
+            above = run;
+        }
+        run += c[b];
+    }
+    const uint64_t who = __ballot(digit >= 0);
+    const int src = __builtin_ctzll(who);
+    need -= (int)__builtin_amdgcn_readlane(above, src);
+    return (uint32_t)__builtin_amdgcn_readlane(digit, src);
+}
+
 // The exact k-th largest (with multiplicity) of the keys a wave holds in registers (0 = empty
 // slot, at least k valid in [klo, khi]), by a radix select in LDS: 8-bit digits from the highest
 // bit in which the valid keys differ. hist: 256 words of LDS used by this wave alone.
@@ -226,29 +254,47 @@ __device__ __forceinline__ uint32_t wave_kth_radix(const uint32_t (&kk)[N], uint
         for (int q = 0; q < N; q++)
             if (kk[q] != 0u && (kk[q] & mask) == prefix) atomicAdd(&hist[(kk[q] >> sh) & dmask], 1u);
         wave_sync();
-        // lane l takes bins 255 - 4l down to 252 - 4l: the counts in descending digit order
-        const u4 h4 = reinterpret_cast<const u4*>(hist)[63 - lane];
-        const uint32_t c[4] = {h4.w, h4.z, h4.y, h4.x};
-        const uint32_t tot = c[0] + c[1] + c[2] + c[3];
-        const uint32_t incl = wave_incl_sum(tot);
-        uint32_t run = incl - tot;  // entries in higher digits than this lane's
-        int digit = -1;
-        uint32_t above = 0;
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            if (digit < 0 && run < (uint32_t)need && run + c[b] >= (uint32_t)need) {
-                digit = 255 - 4 * lane - b;
-                above = run;
-            }
-            run += c[b];
-        }
-        const uint64_t who = __ballot(digit >= 0);
-        const int src = __builtin_ctzll(who);
-        const uint32_t d = (uint32_t)__builtin_amdgcn_readlane(digit, src);
-        need -= (int)__builtin_amdgcn_readlane(above, src);
+        const uint32_t d = hist_digit(hist, lane, need);
         prefix |= d << sh;
         mask |= dmask << sh;
         wave_sync();
+        if (sh == 0) break;
+    }
+    return prefix;
+}
+
+// The exact k-th largest (with multiplicity) of the keys all waves of the workgroup hold in registers
+// (0 = empty slot; at least k valid ones in [klo, khi], the workgroup's smallest and largest valid
+// key), by the same radix select: every wave counts its keys into one LDS histogram, and after the
+// barrier each wave finds the digit from the whole histogram itself (all find the same one), so a
+// digit costs one barrier. Three histograms rotate: while one is filled the next is cleared, and the
+// one before may still be read by a wave that has not reached this digit. The caller clears the
+// first one (h3[0..255]) before a barrier.
+template <int N>
+__device__ __forceinline__ uint32_t block_kth_radix(const uint32_t (&kk)[N], uint32_t klo, uint32_t khi, int k,
+                                                    uint32_t* h3, int t, int lane) {
+    static_assert(kTW == kRB, "one histogram word per thread to clear");
+    if (klo == khi) return khi;
+    const int top = 31 - __clz(klo ^ khi);                        // highest bit that differs
+    uint32_t mask = top == 31 ? 0u : ~((2u << top) - 1u);          // the bits every valid key shares ...
+    uint32_t prefix = khi & mask;                                  // ... and their value
+    int need = k;
+    int cur = 0;
+#pragma unroll 1
+    for (int lo_bit = top - 7;; lo_bit -= 8) {
+        const int sh = lo_bit > 0 ? lo_bit : 0;
+        const uint32_t dmask = (lo_bit >= 0 ? 0xffu : (0xffu >> -lo_bit));
+        uint32_t* hist = h3 + kRB * cur;
+        const int nxt = cur == 2 ? 0 : cur + 1;
+#pragma unroll
+        for (int q = 0; q < N; q++)
+            if (kk[q] != 0u && (kk[q] & mask) == prefix) atomicAdd(&hist[(kk[q] >> sh) & dmask], 1u);
+        h3[kRB * nxt + t] = 0u;
+        __syncthreads();
+        const uint32_t d = hist_digit(hist, lane, need);
+        prefix |= d << sh;
+        mask |= dmask << sh;
+        cur = nxt;
         if (sh == 0) break;
     }
     return prefix;
@@ -1012,23 +1058,65 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
     X.ban = P.ban_id;
     X.invT = invT;
     if (g.t == 0) s.tau_key = 0;
+    // The exact value of entry i: the full transform (penalty, suppression, temperature); entries
+    // past the wave's range (the zeros loaded beyond the row end) are -inf.
+    auto vexact = [&](int i, float x) -> float { return i < hi ? X(i, x) : kNegInf; };
+    // The quarter bounds: a wave with at least kq = ceil(k/4) entries at or above key b_w publishes
+    // b_w (0 = none yet); the four waves' ranges are disjoint, so the row holds at least 4 kq >= k
+    // entries at or above min_w b_w, a lower bound of its k-th largest. A wave's b_w only rises (it
+    // is taken over more of the wave's entries each time). The first ones come from the kPF sweeps
+    // already in registers.
+    const int Kq = (K + 3) / 4;
+    {
+        uint32_t kk[kPF * 4];
+        uint32_t klo = 0xffffffffu, khi = 0;
+        int nf = 0;
+#pragma unroll
+        for (int q = 0; q < kPF; q++) {
+            const float xv[4] = {cur[q].x, cur[q].y, cur[q].z, cur[q].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float v = vexact(lo + q * 256 + 4 * g.lane + j, xv[j]);
+                const bool fin = v > kNegInf;
+                kk[4 * q + j] = fin ? f2key(v) : 0u;
+                klo = fin ? min(klo, kk[4 * q + j]) : klo;
+                khi = fin ? max(khi, kk[4 * q + j]) : khi;
+                nf += __builtin_popcountll(__ballot(fin));
+            }
+        }
+        const uint32_t b = nf >= Kq ? wave_bound_regs(kk, wave_umin(klo), wave_umax(khi), Kq, 16) : 0u;
+        if (g.lane == 0) s.qkey[g.wv] = b;
+    }
     __syncthreads();
 
     // ---- pass A
     uint32_t* wkey = s.wkey[g.wv];
     int32_t* widx = s.widx[g.wv];
     // kStop: the wave stopped collecting (the general algorithm then serves the row); kCompacted: its
-    // buffer was compacted at least once. One word, only ever or-ed: two flag variables had their
-    // stores merged behind a selected address, which kept them in scratch memory.
+    // buffer does not hold every finite entry it has seen (it was compacted, or a bound applied from
+    // the start). One word, only ever or-ed: two flag variables had their stores merged behind a
+    // selected address, which kept them in scratch memory.
     constexpr uint32_t kStop = 1u, kCompacted = 2u;
     uint32_t state = 0;
     int wn = 0;                     // wave-uniform buffer fill
     float tau = -3.402823466e38f;   // entries with fl(x * 1/T) < tau are not candidates ...
-    float xt = x_threshold(tau, invT);  // ... which is x < xt
     float M = kNegInf;              // NaN-propagating maximum of the raw entries
-    // The exact value of entry i: the full transform (penalty, suppression, temperature); entries
-    // past the wave's range (the zeros loaded beyond the row end) are -inf.
-    auto vexact = [&](int i, float x) -> float { return i < hi ? X(i, x) : kNegInf; };
+    auto qmin = [&]() {
+        uint32_t m = 0xffffffffu;
+#pragma unroll
+        for (int w = 0; w < kWW; w++)
+            m = min(m, __hip_atomic_load(&s.qkey[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        return m;
+    };
+    {
+        const uint32_t t0 = qmin();
+        if (t0 != 0u) {
+            tau = key2f(t0);
+            state |= kCompacted;
+            if (g.lane == 0) atomicMax(&s.tau_key, t0);
+        }
+    }
+    float xt = x_threshold(tau, invT);  // entries with x < xt are not candidates
     // Keep the buffered entries whose exact value is >= a lower bound of the k-th largest exact
     // value buffered (one that leaves k to k + 32 of them, ties aside), or the shared bound if that
     // is larger; tau rises to it. With fewer than k finite values buffered the wave stops
@@ -1057,9 +1145,16 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
             state |= kStop;
             return;
         }
-        // a lower bound of the row's k-th largest that keeps at most k + 32 entries (untied)
-        uint32_t kth = wave_bound_regs(kk, wave_umin(klo), wave_umax(khi), K, 32);
-        kth = max(kth, __hip_atomic_load(&s.tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        // a lower bound of the row's k-th largest that keeps at most k + 32 entries (untied), and
+        // this wave's quarter bound (the buffer holds every seen entry at or above its k-th largest)
+        const uint32_t kmax = wave_umax(khi);
+        const uint32_t kown = wave_bound_regs(kk, wave_umin(klo), kmax, K, 32);
+        const uint32_t qb = wave_bound_regs(kk, kown, kmax, Kq, 16);
+        if (g.lane == 0) {
+            atomicMax(&s.qkey[g.wv], qb);
+            atomicMax(&s.tau_key, max(kown, qmin()));
+        }
+        const uint32_t kth = max(kown, __hip_atomic_load(&s.tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
         wave_sync();
         uint32_t m = 0;
 #pragma unroll
@@ -1112,21 +1207,25 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
                     if (wn + cnt > kCapW) state |= kStop;  // ties: the general algorithm
                 }
                 if (cnt == 0 || (state & kStop)) continue;
+                // in index order: a lane's position is the buffer fill plus the candidates of the lower
+                // lanes, counted from the three bits of each lane's count (0..4)
                 const int i0 = base + 4 * g.lane;
+                int c = 0;
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const bool c = xv[j] >= xt;
-                    const uint64_t bal = __ballot(c);
-                    // position: the buffer fill plus the candidates in lower lanes
-                    const uint32_t pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bal, (uint32_t)wn));
-                    if (c) {
+                for (int j = 0; j < 4; j++) c += xv[j] >= xt ? 1 : 0;
+                const uint64_t b0 = __ballot(c & 1), b1 = __ballot(c & 2), b2 = __ballot(c & 4);
+                auto below = [](uint64_t b) {
+                    return __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+                };
+                uint32_t pos = (uint32_t)wn + below(b0) + 2 * below(b1) + 4 * below(b2);
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (xv[j] >= xt) {
                         wkey[pos] = __float_as_uint(xv[j]);
                         widx[pos] = i0 + j;
+                        pos++;
                     }
-                    wn += __builtin_popcountll(bal);
-                }
-                wn = __builtin_amdgcn_readfirstlane(wn);
+                wn = __builtin_amdgcn_readfirstlane(wn + cnt);
             }
             state = __builtin_amdgcn_readfirstlane(state);
             if (state & kStop) break;
@@ -1134,66 +1233,70 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
             for (int q = 0; q < kPF; q++) cur[q] = nxt[q];
         }
     }
-    // the buffered entries as keys of their exact values, keeping the finite ones at or above the
-    // shared bound (a fuller buffer is compacted first, so that the four fit the union's capacity)
-    if (!(state & kStop) && wn > kUnion / kWW) compact();
-    if (!(state & kStop)) {
+    // The buffered entries as keys of their exact values, in registers in index order (slot
+    // lane + 64 q), those below the shared bound dropped (0: no entry). The bound never exceeds the
+    // row's k-th largest, so every entry the reference keeps stays.
+    uint32_t kk[kPerL];
+    int32_t ii[kPerL];
+    uint32_t klo = 0xffffffffu, khi = 0;
+    int nf = 0;
+    {
         wave_sync();
         const uint32_t ts = __hip_atomic_load(&s.tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        uint32_t kk[kPerL];
-        int32_t ii[kPerL];
-        bool fin[kPerL];
 #pragma unroll
         for (int q = 0; q < kPerL; q++) {
             const int j = g.lane + 64 * q;
             ii[q] = widx[j];
-            const bool in = j < wn;
+            const bool in = j < wn && !(state & kStop);
             const float v = vexact(in ? ii[q] : lo, __uint_as_float(wkey[j]));
-            kk[q] = f2key(v);
-            fin[q] = in && v > kNegInf && kk[q] >= ts;
+            const uint32_t key = f2key(v);
+            const bool keep = in && v > kNegInf && key >= ts;
+            kk[q] = keep ? key : 0u;
+            klo = keep ? min(klo, key) : klo;
+            khi = keep ? max(khi, key) : khi;
+            nf += __builtin_popcountll(__ballot(keep));
         }
-        wave_sync();
-        uint32_t m = 0;
-#pragma unroll
-        for (int q = 0; q < kPerL; q++) {
-            const uint64_t bal = __ballot(fin[q]);
-            if (fin[q]) {
-                const uint32_t pos = m + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-                wkey[pos] = kk[q];
-                widx[pos] = ii[q];
-            }
-            m += (uint32_t)__builtin_popcountll(bal);
-        }
-        wave_sync();
-        wn = (int)m;
+        klo = wave_umin(klo);
+        khi = wave_umax(khi);
     }
+    // NaN or fl(M * 1/T) = +inf in a wave's range: the row is checked exactly below
+    const bool wbad = wave_any(M != M || M * invT == kPosInf);
     if (g.lane == 0) {
-        s.wcnt[g.wv] = (state & kStop) ? -1 : wn;
+        s.wcnt[g.wv] = (state & kStop) ? -1 : nf;
         s.wcomp[g.wv] = (state & kCompacted) ? 1 : 0;
+        s.wklo[g.wv] = klo;
+        s.wkhi[g.wv] = khi;
+        s.wbad[g.wv] = wbad ? 1 : 0;
     }
-    // NaN or fl(M * 1/T) = +inf: check the row exactly with the full transform (suppression, or a
-    // penalty, may have removed or lowered that value)
-    bool bad = false;
-    if (g.any(M != M || M * invT == kPosInf))
-        for_row(xrow, V, vec, g.t, X, [&](int, float v) { bad |= __builtin_amdgcn_class(v, 0x203); });
-    if (g.any(bad)) {
-        if (g.t == 0) put_id(a, r, VXS_ERR_NONFINITE);
-        return false;
-    }
-    // The finite count is the buffered total unless some wave compacted, which takes more than k
-    // finite entries (a count of "many" decides top-k the same way).
-    bool all = true, comp = false;
+    s.h.h3[g.t] = 0u;  // the first histogram of the k-th largest select
+    __syncthreads();
+    // The finite count is the buffered total unless some wave's buffer does not hold every finite
+    // entry of its range (compacted, or a bound applied), which takes at least k finite entries (a
+    // count of "many" decides top-k the same way).
+    bool all = true, comp = false, anybad = false;
     uint32_t tot = 0;
+    klo = 0xffffffffu;
+    khi = 0;
 #pragma unroll
     for (int w = 0; w < kWW; w++) {
         all = all && s.wcnt[w] >= 0;
         comp = comp || s.wcomp[w] != 0;
+        anybad = anybad || s.wbad[w] != 0;
         tot += (uint32_t)max(s.wcnt[w], 0);
+        klo = min(klo, s.wklo[w]);
+        khi = max(khi, s.wkhi[w]);
     }
-    if (!all || tot > (uint32_t)kUnion) {  // a wave stopped collecting, or ties fill the buffers
-        return true;  // the general algorithm takes the row
+    // check the row exactly with the full transform (suppression, or a penalty, may have removed or
+    // lowered that value)
+    if (anybad) {
+        bool bad = false;
+        for_row(xrow, V, vec, g.t, X, [&](int, float v) { bad |= __builtin_amdgcn_class(v, 0x203); });
+        if (g.any(bad)) {
+            if (g.t == 0) put_id(a, r, VXS_ERR_NONFINITE);
+            return false;
+        }
     }
+    if (!all) return true;  // a wave stopped collecting: the general algorithm takes the row
     const uint32_t cnt = comp ? (uint32_t)V : tot;
     float* orow = a.out_logits ? a.out_logits + (int64_t)r * V : nullptr;
     double* prow = a.out_probs ? a.out_probs + (int64_t)r * V : nullptr;
@@ -1205,7 +1308,6 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
         return false;
     }
     const bool topk_on = (uint32_t)K < cnt;
-    uint64_t* ckey = reinterpret_cast<uint64_t*>(s.ex.cp);  // (d, index) keys before the probabilities
 
     bool worker = g.wv == 0;  // the wave that runs the sequential tail
     {
@@ -1214,96 +1316,93 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
         for (int w = 0; w < kWW; w++) nw += s.wslot[w];
         if (nw == 1) worker = s.wslot[g.wv] != 0;
     }
-    // ---- the worker wave: k-th largest of the four buffers, the maximum, the candidates
-    if (worker) {
-        // the four buffers, concatenated in order, kSl entries per lane (tot <= kUnion)
-        constexpr int kSl = kUnion / 64;
-        uint32_t kk[kSl];
-        int32_t ii[kSl];
-        uint32_t klo = 0xffffffffu, khi = 0;
-        const int b1 = s.wcnt[0], b2 = b1 + s.wcnt[1], b3 = b2 + s.wcnt[2];
-        const uint32_t* fkey = &s.wkey[0][0];
-        const int32_t* fidx = &s.widx[0][0];
+    // ---- all waves: the k-th largest of the buffered keys, the maximum, the candidates
+    const uint32_t kthkey = topk_on ? block_kth_radix(kk, klo, khi, K, s.h.h3, g.t, g.lane) : 1u;
+    const float mx = key2f(khi);
+    // the candidates (keys >= the k-th largest; 0 < 1 <= every valid key) in index order: the
+    // waves' counts, then each wave writes its own after those of the waves before it
+    {
+        uint32_t mine = 0;
 #pragma unroll
-        for (int q = 0; q < kSl; q++) {
-            const int e = g.lane + 64 * q;
-            const bool in = e < (int)tot;
-            const int j = e < b1 ? e : e < b2 ? kCapW + e - b1 : e < b3 ? 2 * kCapW + e - b2 : 3 * kCapW + e - b3;
-            const int jj = in ? j : 0;  // unconditional reads
-            const uint32_t key = fkey[jj];
-            ii[q] = fidx[jj];
-            kk[q] = in ? key : 0u;  // finite keys are > 0
-            klo = in ? min(klo, key) : klo;
-            khi = in ? max(khi, key) : khi;
-        }
-        khi = wave_umax(khi);
-        const uint32_t kthkey = topk_on ? wave_kth_radix(kk, wave_umin(klo), khi, K, s.h.hcnt, g.lane) : 1u;
-        const float mx = key2f(khi);
-        int n = 0;
+        for (int q = 0; q < kPerL; q++) mine += (uint32_t)__builtin_popcountll(__ballot(kk[q] >= kthkey));
+        if (g.lane == 0) s.wcand[g.wv] = (int32_t)mine;
+    }
+    __syncthreads();
+    int n = 0, off = 0;
 #pragma unroll
-        for (int q = 0; q < kSl; q++) {
+    for (int w = 0; w < kWW; w++) {
+        off += w < g.wv ? s.wcand[w] : 0;
+        n += s.wcand[w];
+    }
+    if (n > kCandW) return true;  // ties beyond the exact-regime capacity: the general algorithm
+    // (d, index) keys, d = v - max, over the wave buffers (every wave has read its own into registers)
+    uint64_t* ckey = reinterpret_cast<uint64_t*>(&s.wkey[0][0]);
+    {
+        uint32_t m = (uint32_t)off;
+#pragma unroll
+        for (int q = 0; q < kPerL; q++) {
             const bool keep = kk[q] >= kthkey;
             const uint64_t bal = __ballot(keep);
-            const int pos = n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-            if (keep && pos < kCandW) {
+            if (keep) {
+                const uint32_t pos = m + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
                 const float v = key2f(kk[q]);
                 s.ex.cx[pos] = v;
                 s.ex.ci[pos] = ii[q];
                 ckey[pos] = ((uint64_t)f2key(v - mx) << 32) | (uint32_t)ii[q];
             }
-            n += __builtin_popcountll(bal);
+            m += (uint32_t)__builtin_popcountll(bal);
         }
-        if (g.lane == 0) {
-            s.n = n;
-            s.kth_key = topk_on ? kthkey : 0u;
-            s.mx = mx;
-        }
+        if (g.t < 8) ckey[n + g.t] = ~0ull;  // above every key: the rank loop reads whole groups of eight
     }
-    __syncthreads();
-    const int n = s.n;
-    const float kth = topk_on ? key2f(s.kth_key) : kNegInf;
-    const float mx = s.mx;
-    if (n > kCandW) {  // ties beyond the exact-regime capacity
-        return true;  // the general algorithm takes the row
-    }
+    const float kth = topk_on ? key2f(kthkey) : kNegInf;
     if (orow) for_row(xrow, V, vec, g.t, X, [&](int i, float x) { orow[i] = x < kth ? kNegInf : x; });
     if (prow)
         for (int i = g.t; i < V; i += kTW) prow[i] = 0.0;
+    __syncthreads();
 
-    // ---- all waves: each candidate's position in index order and in (d, index) order
-    int io = 0, po = 0;
-    float cxt = 0.0f;
-    int32_t cit = 0;
+    // ---- all waves: thread t holds candidate t (index order); its position in (d, index) order,
+    // counted over the keys eight at a time, and its exp(d)                        Sampler.cs:57
     if (g.t < n) {
         const uint64_t kt = ckey[g.t];
-        cxt = s.ex.cx[g.t];
-        cit = s.ex.ci[g.t];
-        // two keys per LDS read; a pair past n reads a stale slot, not counted
         typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
-#pragma unroll 4
-        for (int l = 0; l < n; l += 2) {
-            const u64x2 kl = *reinterpret_cast<const u64x2*>(&ckey[l]);
-            io += (uint32_t)kl.x < (uint32_t)kt ? 1 : 0;
-            po += kl.x < kt ? 1 : 0;
-            io += (l + 1 < n && (uint32_t)kl.y < (uint32_t)kt) ? 1 : 0;
-            po += (l + 1 < n && kl.y < kt) ? 1 : 0;
+        const u64x2* kp = reinterpret_cast<const u64x2*>(ckey);
+        auto below = [&](const u64x2 (&q)[4]) {
+            int c = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) c += (q[k].x < kt ? 1 : 0) + (q[k].y < kt ? 1 : 0);
+            return c;
+        };
+        // the next group's reads are issued before the current group is counted
+        u64x2 ga[4], gb[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) ga[k] = kp[k];
+        int po = 0, l = 8;
+        for (; l + 8 < n; l += 16) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) gb[k] = kp[l / 2 + k];
+            po += below(ga);
+#pragma unroll
+            for (int k = 0; k < 4; k++) ga[k] = kp[l / 2 + 4 + k];
+            po += below(gb);
         }
-    }
-    __syncthreads();
-    if (g.t < n) {
-        s.ex.cx[io] = cxt;
-        s.ex.ci[io] = cit;
-        s.ex.cs[po] = (int16_t)io;
+        if (l < n) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) gb[k] = kp[l / 2 + k];
+            po += below(ga);
+#pragma unroll
+            for (int k = 0; k < 4; k++) ga[k] = gb[k];
+        }
+        po += below(ga);
+        s.ex.cs[po] = (int16_t)g.t;
+        s.ex.cp[g.t] = exp((double)(s.ex.cx[g.t] - mx));
     }
     __syncthreads();
     if (!worker) return false;
 
     // ---- the worker wave: the reference's fp64 arithmetic on the candidates in index order
     double* cp = s.ex.cp;
-    for (int j = g.lane; j < n; j += 64) cp[j] = exp((double)(s.ex.cx[j] - mx));  // Sampler.cs:57
-    wave_sync();
-    const double sum = seq_sum(cp, n);  // sequential in index order                   :58
+    const double sum = seq_sum_pipe(cp, n);  // sequential in index order              :58
     for (int j = g.lane; j < n; j += 64) cp[j] = cp[j] / sum;  //                         :60
     wave_sync();
     if (P.top_p < 1.0f) {  //                                                          :62-75
@@ -1332,16 +1431,42 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
         double* ps = reinterpret_cast<double*>(&s.widx[0][0]);  // p in (p, index) order
         for (int q = g.lane; q < n; q += 64) ps[q] = cp[s.ex.cs[q]];
         wave_sync();
-        const int nrem = wave_topp_cut(ps, n, (double)(1.0f - P.top_p));
+        const int nrem = wave_topp_cut_par(ps, n, (double)(1.0f - P.top_p), g.lane);
         for (int q = g.lane; q < nrem; q += 64) cp[s.ex.cs[q]] = 0.0;
         wave_sync();
-        const double s2 = seq_sum(cp, n);
-        for (int j = g.lane; j < n; j += 64) cp[j] = cp[j] / s2;
+        // The entries left with p > 0 (or NaN), in index order: the second sum and the draw over
+        // them alone are the reference's over all n (adding zero changes no sum; the draw skips
+        // p <= 0).
+        double* kp = ps;  // the sorted copy is no longer needed
+        int32_t* kid = &s.widx[2][0];
+        int nk = 0;
+        for (int b = 0; b < n; b += 64) {
+            const int j = b + g.lane;
+            const double pj = j < n ? cp[j] : 0.0;
+            const bool keep = j < n && !(pj <= 0.0);
+            const uint64_t bal = __ballot(keep);
+            if (keep) {
+                const int pos = nk + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+                kp[pos] = pj;
+                kid[pos] = s.ex.ci[j];
+            }
+            nk += __builtin_popcountll(bal);
+        }
         wave_sync();
+        const double s2 = seq_sum(kp, nk);  // probs.Sum() in index order               :73
+        for (int q = g.lane; q < nk; q += 64) kp[q] = kp[q] / s2;  //                  :74
+        if (prow)
+            for (int j = g.lane; j < n; j += 64) cp[j] = cp[j] / s2;
+        wave_sync();
+        const double u = row_uniform(a, r);
+        const int pick = wave_draw(kp, kid, nk, u);  // inverse-CDF draw in index order :77-87
+        if (g.lane == 0) put_id(a, r, pick);
+    } else {
+        const double u = row_uniform(a, r);
+        const int pick = wave_draw(cp, s.ex.ci, n, u);  // inverse-CDF draw in index order :77-87
+        if (g.lane == 0) put_id(a, r, pick);
     }
-    const double u = row_uniform(a, r);
-    const int pick = wave_draw(cp, s.ex.ci, n, u);  // inverse-CDF draw in index order :77-87
-    if (g.lane == 0) put_id(a, r, pick);
     if (prow)
         for (int j = g.lane; j < n; j += 64) prow[s.ex.ci[j]] = cp[j];
     return false;
