@@ -136,6 +136,32 @@ def test_wide_topp_ranks_by_probability_on_near_ties(ctx):
     check_rows(ctx, x, p, np.linspace(0.03, 0.97, rows), label="wide near ties")
 
 
+def test_wide_topp_threshold_on_a_prefix_sum(ctx):
+    """Top-p thresholds equal to a running sum of the sorted probabilities (m equal candidates, so
+    every p is 1/m exactly and 1 - top_p lands on a prefix sum): the cut is decided by cum <= thr
+    with equality, where the kernel's parallel prefix sums cannot decide and its sequential form
+    must. Also thresholds just above and below such a sum, and rows whose candidates all survive."""
+    rows, vocab = 12, 20000
+    rng = np.random.default_rng(77)
+    x = np.full((rows, vocab), -2000.0, np.float32)  # exp(x - max) underflows to 0 in double
+    m = [4, 8, 8, 16, 4, 4, 32, 2, 64, 8, 128, 256]
+    top_p = [0.75, 0.5, 0.625, 0.75, 0.7500001, 0.7499999, 0.875, 0.5, 0.9375, 0.9999999, 0.5, 0.25]
+    for r in range(rows):
+        cols = rng.choice(vocab, size=m[r], replace=False)
+        x[r, cols] = 10.0
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = 1
+    p["top_k"] = m
+    p["top_p"] = np.array(top_p, np.float32)
+    p["temperature"] = 1.0
+    p["rep_penalty"] = 1.0
+    p["keep_id"] = -1
+    p["ban_id"] = -1
+    for u in (np.linspace(0.01, 0.99, rows), np.full(rows, 0.5)):
+        ids, ora = check_rows(ctx, x, p, u, label="wide top-p on a prefix sum")
+        assert (ids >= 0).all()
+
+
 def test_wide_handback_next_to_ordered_rows(ctx):
     """Rows of the wide workload's options (top-k 200, penalty, suppression) next to rows the ordered
     pass must hand back to the general algorithm in the same workgroup: 2000 entries tied at the
