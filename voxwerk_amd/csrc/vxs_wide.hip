@@ -483,11 +483,13 @@ __device__ __forceinline__ void wide_general_row(const SampleArgs& a, int vec, i
     int bi = 0x7fffffff;
     bool bad = false;
     uint32_t ninf = 0;  // wave-uniform count of -inf entries
-    // Raw buffer loads bounded by the row: lanes past its end read zeros instead of faulting, so
-    // every sweep is one branch-free 16-byte load per lane (entries at or past `hi` are masked).
+    // Raw buffer loads bounded by the end of the wave's range: loads past it read zeros without
+    // fetching (lanes past the row end, the prefetch beyond the range), so every sweep is one
+    // branch-free 16-byte load per lane (entries at or past `hi` are masked) and the next wave's
+    // entries are not fetched twice.
     typedef float f4 __attribute__((ext_vector_type(4)));
     const __amdgpu_buffer_rsrc_t rowbuf =
-        __builtin_amdgcn_make_buffer_rsrc((void*)xrow, (short)0, V * (int)sizeof(float), 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc((void*)xrow, (short)0, hi * (int)sizeof(float), 0x00020000);
     auto load4 = [&](int base) -> f4 {
         return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rowbuf, (base + 4 * g.lane) * 4, 0, 2));
     };
@@ -1031,9 +1033,11 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
     const int Q = ((V + kTW * 4 - 1) / (kTW * 4)) * 256;  // a wave's range, a multiple of 256
     const int lo = g.wv * Q, hi = min(V, lo + Q);
     typedef float f4 __attribute__((ext_vector_type(4)));
-    // raw buffer loads bounded by the row: lanes past its end read zeros instead of faulting
+    // raw buffer loads bounded by the end of the wave's range: loads past it (the prefetch beyond the
+    // range, lanes past the row end) read zeros without fetching, so the next wave's entries are
+    // not fetched twice
     const __amdgpu_buffer_rsrc_t rowbuf =
-        __builtin_amdgcn_make_buffer_rsrc((void*)xrow, (short)0, V * (int)sizeof(float), 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc((void*)xrow, (short)0, hi * (int)sizeof(float), 0x00020000);
     auto load4 = [&](int base) -> f4 {
         return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rowbuf, (base + 4 * g.lane) * 4, 0, 2));
     };
