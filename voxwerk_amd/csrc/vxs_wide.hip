@@ -996,22 +996,27 @@ __device__ __forceinline__ float x_threshold(float tau, float invT) {
 // The ordered pass: the rows row_ordered() selects, in one read of the row. Returns true when the
 // general algorithm must serve the row instead.
 //
-// Pass A: each wave streams its quarter of the row and keeps a buffer of raw values and indices.
-// The exact transformed value v (penalty, suppression, temperature) is at most fl(x * 1/T), which
-// is monotone in the raw x, so an entry joins the buffer when x >= xt, the smallest float with
-// fl(xt * 1/T) >= tau: one compare per entry. Whenever the buffer cannot take a sweep's entries,
-// the exact values of the buffered entries are formed (suppressed entries and those past the
-// wave's range become -inf) and the buffer is cut to a lower bound of its k-th largest (k to
-// k + 32 entries stay), which becomes tau: a lower bound of the row's k-th largest, shared between
-// the waves. NaN and +inf reach the NaN-propagating maximum M of the raw values; M NaN or
-// fl(M * 1/T) = +inf sends the row through an exact check with the full transform (suppression
-// or the penalty may have removed or lowered that value).
-// Tail: one wave finds the k-th largest of the four buffers by a radix select and extracts the
-// candidates; all waves rank them by index and by (d, index), d = v - max; that wave runs the
-// reference's sequential fp64 arithmetic (S6-S8, Sampler.cs:51-87). The (d, index) order is the
-// reference's (p, index) order whenever each adjacent pair is in (p, index) order (p = exp(d) / sum
-// never decreases with d for a monotone exp); otherwise the candidates are ranked by p directly.
-// Rows that end with too many tied candidates go to the general algorithm.
+// Pass A: each wave streams its quarter of the row and keeps a buffer of raw values and indices,
+// in index order. The exact transformed value v (penalty, suppression, temperature) is at most
+// fl(x * 1/T), which is monotone in the raw x, so an entry joins the buffer when x >= xt, the
+// smallest float with fl(xt * 1/T) >= tau: one compare per entry. tau is a lower bound of the row's
+// k-th largest, shared between the waves, from two rules: whenever a wave's buffer cannot take a
+// sweep's entries, the exact values of its entries are formed (suppressed entries and those past
+// the wave's range become -inf) and the buffer is cut to a lower bound of its k-th largest (k to
+// k + 32 entries stay); and each wave publishes a key with at least ceil(k/4) of its entries at or
+// above it (first from the sweeps in registers before the stream starts), so the smallest of the
+// four has at least k of the row's entries at or above it. NaN and +inf reach the NaN-propagating
+// maximum M of the raw values; M NaN or fl(M * 1/T) = +inf sends the row through an exact check
+// with the full transform (suppression or the penalty may have removed or lowered that value).
+// Tail: the four waves hold their buffers' exact keys in registers; a radix select over all of them
+// (block_kth_radix) gives the row's k-th largest; the candidates are written in index order; each
+// thread ranks its candidate by (d, index), d = v - max, and forms exp(d); one wave runs the
+// reference's sequential fp64 arithmetic (S6-S8, Sampler.cs:51-87), its top-p cut from a wave scan
+// checked against a rounding bound (wave_topp_cut_par) and its second sum and draw over the kept
+// entries only. The (d, index) order is the reference's (p, index) order whenever each adjacent pair
+// is in (p, index) order (p = exp(d) / sum never decreases with d for a monotone exp); otherwise the
+// candidates are ranked by p directly. Rows that end with too many tied candidates go to the general
+// algorithm.
 // =====================================================================================
 __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, int r, BlkW& g, WideSmem& s,
                                                  uint32_t* bm_dyn) {
