@@ -528,51 +528,76 @@ __device__ __forceinline__ int wave_exact(float x, const int32_t* ids, int n, fl
     double p = in ? exp((double)(x - m)) : 0.0;  // :57, x - m in fp32, then Math.Exp
     cp[lane] = p;
     wave_lds_sync();
-    p = in ? p / seq_sum(cp, n) : 0.0;  // :58-60, the sum in index order
-    if (topp) {  // :62-75
-        // Stable ascending (p, index) order. p = exp(d) / sum never decreases with d = fl32(x - m),
-        // so the (d, index) order is taken when every adjacent pair of it is in (p, index) order,
-        // else the entries are ranked by p directly.
-        const uint64_t k = in ? ((uint64_t)f2key(x - m) << 32) | (uint32_t)lane : ~0ull;
-        key[lane] = k;
+    p = in ? p / seq_sum_pipe(cp, n) : 0.0;  // :58-60, the sum in index order
+    if (!topp) {
+        if (prow && in) prow[ids[lane]] = p;
         cp[lane] = p;
         wave_lds_sync();
-        int rank = 0;
-#pragma unroll 8
-        for (int l = 0; l < n; l++) rank += key[l] < k ? 1 : 0;
-        wave_lds_sync();  // every lane has read the keys
-        int* at = reinterpret_cast<int*>(key);
-        if (in) {
-            ps[rank] = p;
-            at[rank] = lane;
-        }
-        wave_lds_sync();
-        const bool has_next = in && rank + 1 < n;
-        const double pn = ps[has_next ? rank + 1 : 0];
-        const int ln = at[has_next ? rank + 1 : 0];
-        if (__ballot(has_next && !(p < pn || (p == pn && lane < ln)))) {
-            rank = 0;
-#pragma unroll 8
-            for (int l = 0; l < n; l++) {
-                const double pl = cp[l];
-                rank += (pl < p || (pl == p && l < lane)) ? 1 : 0;
-            }
-            wave_lds_sync();  // every lane has read ps above
-            if (in) ps[rank] = p;
-            wave_lds_sync();
-        }
-        // positions 0 .. n - 2 are removed while the running sum stays <= 1 - top_p
-        const int nrem = wave_topp_cut(ps, n, (double)(1.0f - top_p));
-        if (in && rank < nrem) p = 0.0;
-        wave_lds_sync();  // the cut has read ps
-        cp[lane] = p;
-        wave_lds_sync();
-        p = in ? p / seq_sum(cp, n) : 0.0;  // probs.Sum() in index order, then :74
+        return wave_draw(cp, ids, n, u);  // :77-87
     }
-    if (prow && in) prow[ids[lane]] = p;
+    // :62-75. Stable ascending (p, index) order. p = exp(d) / sum never decreases with
+    // d = fl32(x - m), so the (d, index) order is taken when every adjacent pair of it is in
+    // (p, index) order, else the entries are ranked by p directly.
+    const uint64_t k = in ? ((uint64_t)f2key(x - m) << 32) | (uint32_t)lane : ~0ull;
+    key[lane] = k;
+    if (lane == 0) key[n] = ~0ull;  // above every key: the rank loop reads pairs
     cp[lane] = p;
     wave_lds_sync();
-    return wave_draw(cp, ids, n, u);  // :77-87
+    int rank = 0;
+    {
+        typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
+        const u64x2* kp = reinterpret_cast<const u64x2*>(key);
+#pragma unroll 4
+        for (int l = 0; l < n; l += 2) {
+            const u64x2 q = kp[l / 2];
+            rank += (q.x < k ? 1 : 0) + (q.y < k ? 1 : 0);
+        }
+    }
+    wave_lds_sync();  // every lane has read the keys
+    int* at = reinterpret_cast<int*>(key);
+    if (in) {
+        ps[rank] = p;
+        at[rank] = lane;
+    }
+    wave_lds_sync();
+    const bool has_next = in && rank + 1 < n;
+    const double pn = ps[has_next ? rank + 1 : 0];
+    const int ln = at[has_next ? rank + 1 : 0];
+    if (__ballot(has_next && !(p < pn || (p == pn && lane < ln)))) {
+        rank = 0;
+#pragma unroll 8
+        for (int l = 0; l < n; l++) {
+            const double pl = cp[l];
+            rank += (pl < p || (pl == p && l < lane)) ? 1 : 0;
+        }
+        wave_lds_sync();  // every lane has read ps above
+        if (in) ps[rank] = p;
+        wave_lds_sync();
+    }
+    // positions 0 .. n - 2 are removed while the running sum stays <= 1 - top_p
+    const int nrem = wave_topp_cut_par(ps, n, (double)(1.0f - top_p), lane);
+    if (in && rank < nrem) p = 0.0;
+    // The entries left with p > 0 (or NaN), in index order: the second sum and the draw over them
+    // alone are the reference's over all n (adding zero changes no sum; the draw skips p <= 0).
+    const bool keep = in && !(p <= 0.0);
+    const uint64_t kb = __ballot(keep);
+    const int nk = (int)__builtin_popcountll(kb);
+    const int pos = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(kb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)kb, 0u));
+    double* kp = ps;  // the cut has read ps (its result is uniform, so every lane is past it)
+    int32_t* kid = reinterpret_cast<int32_t*>(key);
+    wave_lds_sync();
+    if (keep) {
+        kp[pos] = p;
+        kid[pos] = ids[lane];
+    }
+    wave_lds_sync();
+    const double s2 = seq_sum(kp, nk);  // probs.Sum() in index order
+    p = in ? p / s2 : 0.0;              // :74
+    if (prow && in) prow[ids[lane]] = p;
+    wave_lds_sync();  // every lane has read kp
+    if (keep) kp[pos] = p;
+    wave_lds_sync();
+    return wave_draw(kp, kid, nk, u);  // :77-87
 }
 
 // Stable ascending (p, index) rank of entry j among p[0..n).
