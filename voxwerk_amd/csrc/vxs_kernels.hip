@@ -192,11 +192,11 @@ struct Ctl {
 
 template <int NC>
 struct RowSmem {
+    float tmax[kT];  // the threads' largest values (published with the row statistics, read by top-k)
     using C = Cfg<NC>;
     uint32_t bm[C::BMW];
     union {
         float xs[C::VMAX];  // staged row for the penalty
-        float tmax[kT];     // top-k: the threads' largest values
         struct {
             double hist[kNB];
             uint32_t lkey[kLMax];
@@ -710,6 +710,7 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
             tmx = fmaxf(tmx, v[e]);
             tmn = fminf(tmn, v[e]);
         }
+        sm.tmax[g.t] = tmx;
         const float wmx = wave_fmax(tmx);
         const float wmn = wave_fmin(tmn);
         if (g.lane == 0) {
@@ -763,20 +764,15 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
         // the row) are >= T, and at most K + 32 unless ties force more. When the entries >= T
         // fit the exact-regime capacity they are the candidates: all entries >= the k-th largest
         // are among them, so their own k-th largest is the row's.
-        float tm = kNegInf;
-#pragma unroll
-        for (int e = 0; e < NE; e++) tm = fmaxf(tm, v[e]);
-        sm.u.tmax[g.t] = tm;
-        g.sync();
         uint32_t mk[kT / 64];
         uint32_t mlo = 0xffffffffu, mhi = 0;
 #pragma unroll
         for (int q = 0; q < kT / 64; q++) {
-            mk[q] = f2key(sm.u.tmax[g.lane + 64 * q]);
+            mk[q] = f2key(sm.tmax[g.lane + 64 * q]);
             mlo = min(mlo, mk[q]);
             mhi = max(mhi, mk[q]);
         }
-        const float Tb = key2f(wave_bound_regs(mk, wave_umin(mlo), wave_umax(mhi), K, 32));
+        const float Tb = key2f(wave_bound_regs4(mk, wave_umin(mlo), wave_umax(mhi), K, 32));
         // the entries >= Tb in index order: 16-bit counts per sweep, four sweeps per scan
         auto& ex = sm.u.ex;
         uint32_t tot = 0;

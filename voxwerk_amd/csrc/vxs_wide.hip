@@ -206,100 +206,6 @@ __device__ __forceinline__ uint32_t wave_kth_regs(const uint32_t (&kk)[N], uint3
     return lo;
 }
 
-// The digit of the need-th largest counted key, from a 256-bin histogram of the current digit read
-// by one wave (lane l takes bins 255 - 4l down to 252 - 4l, the counts in descending digit order);
-// need drops by the count of keys in higher digits.
-__device__ __forceinline__ uint32_t hist_digit(const uint32_t* hist, int lane, int& need) {
-    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-    const u4 h4 = reinterpret_cast<const u4*>(hist)[63 - lane];
-    const uint32_t c[4] = {h4.w, h4.z, h4.y, h4.x};
-    const uint32_t tot = c[0] + c[1] + c[2] + c[3];
-    const uint32_t incl = wave_incl_sum(tot);
-    uint32_t run = incl - tot;  // entries in higher digits than this lane's
-    int digit = -1;
-    uint32_t above = 0;
-#pragma unroll
-    for (int b = 0; b < 4; b++) {
-        if (digit < 0 && run < (uint32_t)need && run + c[b] >= (uint32_t)need) {
-            digit = 255 - 4 * lane - b;
-            above = run;
-        }
-        run += c[b];
-    }
-    const uint64_t who = __ballot(digit >= 0);
-    const int src = __builtin_ctzll(who);
-    need -= (int)__builtin_amdgcn_readlane(above, src);
-    return (uint32_t)__builtin_amdgcn_readlane(digit, src);
-}
-
-// The exact k-th largest (with multiplicity) of the keys a wave holds in registers (0 = empty
-// slot, at least k valid in [klo, khi]), by a radix select in LDS: 8-bit digits from the highest
-// bit in which the valid keys differ. hist: 256 words of LDS used by this wave alone.
-template <int N>
-__device__ __forceinline__ uint32_t wave_kth_radix(const uint32_t (&kk)[N], uint32_t klo, uint32_t khi, int k,
-                                                   uint32_t* hist, int lane) {
-    if (klo == khi) return khi;
-    const int top = 31 - __clz(klo ^ khi);                        // highest bit that differs
-    uint32_t mask = top == 31 ? 0u : ~((2u << top) - 1u);          // the bits every valid key shares ...
-    uint32_t prefix = khi & mask;                                  // ... and their value
-    int need = k;
-    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-#pragma unroll 1
-    for (int lo_bit = top - 7;; lo_bit -= 8) {
-        const int sh = lo_bit > 0 ? lo_bit : 0;
-        const uint32_t dmask = (lo_bit >= 0 ? 0xffu : (0xffu >> -lo_bit));
-        reinterpret_cast<u4*>(hist)[lane] = u4{0u, 0u, 0u, 0u};
-        wave_sync();
-#pragma unroll
-        for (int q = 0; q < N; q++)
-            if (kk[q] != 0u && (kk[q] & mask) == prefix) atomicAdd(&hist[(kk[q] >> sh) & dmask], 1u);
-        wave_sync();
-        const uint32_t d = hist_digit(hist, lane, need);
-        prefix |= d << sh;
-        mask |= dmask << sh;
-        wave_sync();
-        if (sh == 0) break;
-    }
-    return prefix;
-}
-
-// The exact k-th largest (with multiplicity) of the keys all waves of the workgroup hold in registers
-// (0 = empty slot; at least k valid ones in [klo, khi], the workgroup's smallest and largest valid
-// key), by the same radix select: every wave counts its keys into one LDS histogram, and after the
-// barrier each wave finds the digit from the whole histogram itself (all find the same one), so a
-// digit costs one barrier. Three histograms rotate: while one is filled the next is cleared, and the
-// one before may still be read by a wave that has not reached this digit. The caller clears the
-// first one (h3[0..255]) before a barrier.
-template <int N>
-__device__ __forceinline__ uint32_t block_kth_radix(const uint32_t (&kk)[N], uint32_t klo, uint32_t khi, int k,
-                                                    uint32_t* h3, int t, int lane) {
-    static_assert(kTW == kRB, "one histogram word per thread to clear");
-    if (klo == khi) return khi;
-    const int top = 31 - __clz(klo ^ khi);                        // highest bit that differs
-    uint32_t mask = top == 31 ? 0u : ~((2u << top) - 1u);          // the bits every valid key shares ...
-    uint32_t prefix = khi & mask;                                  // ... and their value
-    int need = k;
-    int cur = 0;
-#pragma unroll 1
-    for (int lo_bit = top - 7;; lo_bit -= 8) {
-        const int sh = lo_bit > 0 ? lo_bit : 0;
-        const uint32_t dmask = (lo_bit >= 0 ? 0xffu : (0xffu >> -lo_bit));
-        uint32_t* hist = h3 + kRB * cur;
-        const int nxt = cur == 2 ? 0 : cur + 1;
-#pragma unroll
-        for (int q = 0; q < N; q++)
-            if (kk[q] != 0u && (kk[q] & mask) == prefix) atomicAdd(&hist[(kk[q] >> sh) & dmask], 1u);
-        h3[kRB * nxt + t] = 0u;
-        __syncthreads();
-        const uint32_t d = hist_digit(hist, lane, need);
-        prefix |= d << sh;
-        mask |= dmask << sh;
-        cur = nxt;
-        if (sh == 0) break;
-    }
-    return prefix;
-}
-
 // k-th largest (1-based, with multiplicity) of a wave's n >= k buffered keys; wave-local.
 __device__ __forceinline__ uint32_t wave_kth(const uint32_t* keys, int lane, int n, int k) {
     uint32_t kk[kPerL];
