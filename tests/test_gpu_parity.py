@@ -162,6 +162,39 @@ def test_history_id_out_of_range(ctx):
         ctx.sample(x, p, np.array([0.5, 0.5]), off, hist)
 
 
+@pytest.mark.parametrize("vocab", [3072, 8192])
+def test_long_histories_block_path(ctx, vocab):
+    """Histories around and past the 2048 ids a workgroup takes in one pass (the rest go through the
+    bitmap), with ids repeated within and across the two parts, on the one-workgroup kernel; then an
+    id out of range in each part."""
+    rng = np.random.default_rng(9000 + vocab)
+    lens = [0, 1, 2047, 2048, 2049, 3000, 6000, 9000]
+    rows = len(lens)
+    x = (rng.standard_normal((rows, vocab)) * 2.0).astype(np.float32)
+    off = np.zeros(rows + 1, np.int32)
+    off[1:] = np.cumsum(lens)
+    pool = rng.integers(0, vocab, size=700)  # few distinct ids: most are repeats
+    hist = pool[rng.integers(0, pool.size, size=off[-1])].astype(np.int32)
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = 1
+    p["top_k"] = [0, 50, 0, 50, 0, 50, 0, 50]
+    p["top_p"] = np.float32(0.9)
+    p["temperature"] = np.float32(0.9)
+    p["rep_penalty"] = np.array([1.1, 0.9] * 4, np.float32)
+    p["keep_id"] = -1
+    p["ban_id"] = -1
+    u = rng.random(rows)
+    ids, lg, pr = ctx.sample(x, p, u, off, hist, want_logits=True, want_probs=True, path="block")
+    ora = ref.sample(x, p, u, off, hist, threads=8, want_logits=True, want_probs=True)
+    check(ids, lg, pr, ora, label=f"long histories V={vocab}")
+    for at in (100, 2500):  # in the first 2048 ids of the 3000-id row, then past them
+        bad = hist.copy()
+        bad[off[5] + at] = vocab
+        got = ctx.sample(x, p, u, off, bad, raise_on_error=False, path="block")
+        assert got[5] == -2, (at, got[5])
+        assert np.array_equal(np.delete(got, 5), np.delete(ids, 5))
+
+
 def test_nonfinite_rejected(ctx):
     x = np.zeros((3, 1024), np.float32)
     x[0, 5] = np.nan

@@ -60,6 +60,7 @@ struct Cfg {
 // refinement loop reuses its sites with an explicit barrier.
 enum Site : int {
     kSiteErr,
+    kSiteErr2,
     kSiteNan,
     kSiteArgV,
     kSiteArgI,
@@ -559,59 +560,68 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
         const float rinv = 1.0f / rho;
         const float arho = __builtin_fabsf(rho);
         const bool fast = arho >= 0x1p-60f && arho <= 0x1p60f;
-        bool bad = false;
-        // The row is staged in LDS; the thread whose atomicOr first sets an id's bit owns the id and
-        // rescales that logit in place, then every thread reloads its elements.
+        // The row is staged in LDS. The first HP * kT ids (prefetched with the row): every thread
+        // reads the staged logit of each of its ids, the workgroup synchronises, then every thread
+        // writes the penalised value back, so a repeated id writes the same value again and each
+        // distinct id is penalised once, with no atomics. A longer history marks those ids in an LDS
+        // bitmap, and the thread whose atomicOr first sets a later id's bit rescales that one. Then
+        // every thread reloads its elements.
         float* xs = sm.u.xs;
         typedef float f4 __attribute__((ext_vector_type(4)));
 #pragma unroll
         for (int c = 0; c < NC; c++)
             *(f4*)(xs + c * kSW + g.t * 4) = f4{v[c * 4 + 0], v[c * 4 + 1], v[c * 4 + 2], v[c * 4 + 3]};
-        for (int w = g.t; w < C::BMW; w += kT) sm.bm[w] = 0;
+        const bool longer = h1 - h0 > HP * kT;  // uniform
+        if (longer)
+            for (int w = g.t; w < C::BMW; w += kT) sm.bm[w] = 0;
         g.sync();
-        auto own = [&](int id) {
-            if ((unsigned)id >= (unsigned)V) {
-                bad = true;
-                return;
-            }
-            const uint32_t bit = 1u << (id & 31);
-            if (!(atomicOr(&sm.bm[id >> 5], bit) & bit)) xs[id] = penalize(xs[id], rho, rinv, fast);
-        };
-        {
-            // the prefetched ids: every bitmap atomic issued before any owner rescales its logit
-            // (an id's owner is unique, so the rescales touch distinct entries)
-            uint32_t won = 0;
+        bool live[HP];
+        float xv[HP];
+        bool bad = false;
 #pragma unroll
-            for (int k = 0; k < HP; k++) {
-                const int id = pre[k];
-                const bool in = h0 + g.t + k * kT < h1;
-                if (in && (unsigned)id >= (unsigned)V) bad = true;
-                if (in && (unsigned)id < (unsigned)V) {
-                    const uint32_t bit = 1u << (id & 31);
-                    won |= (atomicOr(&sm.bm[id >> 5], bit) & bit) ? 0u : 1u << k;
-                }
-            }
-            float xv[HP];
-#pragma unroll
-            for (int k = 0; k < HP; k++) xv[k] = (won >> k) & 1u ? xs[pre[k]] : 0.0f;
-#pragma unroll
-            for (int k = 0; k < HP; k++)
-                if ((won >> k) & 1u) xs[pre[k]] = penalize(xv[k], rho, rinv, fast);
+        for (int k = 0; k < HP; k++) {
+            const bool in = h0 + g.t + k * kT < h1;
+            bad |= in && (unsigned)pre[k] >= (unsigned)V;
+            live[k] = in && (unsigned)pre[k] < (unsigned)V;
+            xv[k] = live[k] ? xs[pre[k]] : 0.0f;
         }
-        for (int hb = h0 + HP * kT; hb < h1; hb += 4 * kT) {  // the rest, four ids per thread in flight
-            int id[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int h = hb + k * kT + g.t;
-                id[k] = h < h1 ? a.hist_ids[h] : 0;
-            }
-#pragma unroll
-            for (int k = 0; k < 4; k++)
-                if (hb + k * kT + g.t < h1) own(id[k]);
-        }
-        if (g.any(bad, kSiteErr)) {
+        if (g.any(bad, kSiteErr)) {  // its barrier also orders every read above before the writes
             if (g.t == 0) put_id(a, r, VXS_ERR_ID_OUT_OF_RANGE);
             return;
+        }
+#pragma unroll
+        for (int k = 0; k < HP; k++)
+            if (live[k]) xs[pre[k]] = penalize(xv[k], rho, rinv, fast);
+        if (longer) {
+#pragma unroll
+            for (int k = 0; k < HP; k++)
+                if (live[k]) atomicOr(&sm.bm[pre[k] >> 5], 1u << (pre[k] & 31));
+            g.sync();
+            auto own = [&](int id) {
+                if ((unsigned)id >= (unsigned)V) {
+                    bad = true;
+                    return;
+                }
+                const uint32_t bit = 1u << (id & 31);
+                if (!(atomicOr(&sm.bm[id >> 5], bit) & bit)) xs[id] = penalize(xs[id], rho, rinv, fast);
+            };
+            for (int hb = h0 + HP * kT; hb < h1; hb += 4 * kT) {  // four ids per thread in flight
+                int id[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int h = hb + k * kT + g.t;
+                    id[k] = h < h1 ? a.hist_ids[h] : 0;
+                }
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    if (hb + k * kT + g.t < h1) own(id[k]);
+            }
+            if (g.any(bad, kSiteErr2)) {
+                if (g.t == 0) put_id(a, r, VXS_ERR_ID_OUT_OF_RANGE);
+                return;
+            }
+        } else {
+            g.sync();  // every write above lands before the reload
         }
 #pragma unroll
         for (int c = 0; c < NC; c++) {
