@@ -521,24 +521,25 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
 
     // ---- the row loads first, then the options and the history range (independent of each
     // other, so that inputs read over PCIe cost one round trip before the history ids)
+    // No lane branches around these loads: a divergent branch runs both sides under exec masks,
+    // and the compiler then waits for the loads of one side before the other side's next load,
+    // which puts one round trip per sweep on a row read over PCIe.
     float v[NE];
 #pragma unroll
     for (int c = 0; c < NC; c++) {
         const int i0 = c * kSW + g.t * 4;
-        if (vec && i0 + 3 < V) {
+        if (vec && (c + 1) * kSW <= V) {  // uniform: a full sweep, one aligned quad per thread
             typedef float f4 __attribute__((ext_vector_type(4)));
             const f4 q = __builtin_nontemporal_load((const f4*)(xrow + i0));
             v[c * 4 + 0] = q.x;
             v[c * 4 + 1] = q.y;
             v[c * 4 + 2] = q.z;
             v[c * 4 + 3] = q.w;
-        } else {
+        } else {  // unaligned rows and the partial last sweep: element loads at in-row addresses
 #pragma unroll
-            for (int j = 0; j < 4; j++) v[c * 4 + j] = (i0 + j < V) ? xrow[i0 + j] : kNegInf;
+            for (int j = 0; j < 4; j++) v[c * 4 + j] = xrow[min(i0 + j, V - 1)];
         }
     }
-    // entries past the vocabulary (pads of the last sweep) hold -inf: they never win, carry no mass
-    // and are never written back
     const vxs_params P = a.params[(int64_t)r * a.params_stride];
     HistRange hr{0, 0};
     if (has_history(a)) hr = history_range(a, r);
@@ -553,6 +554,11 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
             pre[k] = h < h1 ? a.hist_ids[h] : 0;
         }
     }
+    // entries past the vocabulary (pads of the last sweep) hold -inf: they never win, carry no mass
+    // and are never written back (masked here, with the loads above all in flight)
+#pragma unroll
+    for (int e = 0; e < NE; e++)
+        if ((e >> 2) * kSW + kSW > V && eidx(e) >= V) v[e] = kNegInf;
 
     // ---- S1: repetition penalty over the distinct history ids
     if (pen_on && h1 > h0) {
