@@ -150,32 +150,46 @@ def measure_frame_embedding(ctx, rows: int, steps: int, hip, np) -> dict:
             "pct_of_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2)}
 
 
-def measure_head(ctx, rows: int, k: int, n: int, steps: int, hip, np) -> dict:
-    """vxs_head_device (rows x k fp32 times a bf16 [n][k] weight), HIP events on the context stream.
-    The weight is rotated over enough copies to miss the last-level cache, so every launch reads it
-    from HBM. Algorithmic bytes: the weight (2 n k), the hidden rows (4 rows k) and the logits."""
+def measure_head(ctx, rows: int, k: int, n: int, steps: int, hip, np, int8: bool = False) -> dict:
+    """vxs_head_device (rows x k fp32 times a bf16 [n][k] weight), or with int8 vxs_head_int8_device
+    (an int8 [n][k] weight packed on the device by vxs_head_pack_int8_device, and its n scales), HIP
+    events on the context stream. The weight is rotated over enough copies to miss the last-level
+    cache, so every launch reads it from HBM. Algorithmic bytes: the weight (2 n k, or n k + 4 n),
+    the hidden rows (4 rows k) and the logits (4 rows n)."""
     rng = np.random.default_rng(4)
-    w_bytes = 2 * n * k
+    w_bytes = (n * k + 4 * n) if int8 else 2 * n * k
     nbuf = max(2, math.ceil(2 * LLC_BYTES / w_bytes) + 1)
     w0 = (rng.standard_normal((n, k)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
-    d_w = [hip.DeviceArray.from_numpy(w0) for _ in range(nbuf)]
+    d_w = [hip.DeviceArray.from_numpy(w0) for _ in range(1 if int8 else nbuf)]
+    d_q = [hip.DeviceArray((n, k), np.int8) for _ in range(nbuf)] if int8 else []
+    d_s = [hip.DeviceArray((n,), np.float32) for _ in range(nbuf)] if int8 else []
+    for q, s in zip(d_q, d_s):
+        ctx.head_pack_int8_device(k, n, d_w[0], k, q, k, s)
     d_x = hip.DeviceArray.from_numpy(rng.standard_normal((rows, k)).astype(np.float32))
     d_o = hip.DeviceArray((rows, n), np.float32)
+
+    def launch(i):
+        if int8:
+            ctx.head_int8_device(rows, k, n, d_x, k, d_q[i % nbuf], k, d_s[i % nbuf], d_o, n)
+        else:
+            ctx.head_device(rows, k, n, d_x, k, d_w[i % nbuf], k, d_o, n)
+
     for i in range(20):
-        ctx.head_device(rows, k, n, d_x, k, d_w[i % nbuf], k, d_o, n)
+        launch(i)
     hip.synchronize()
     e0, e1 = hip.Event(), hip.Event()
     e0.record(ctx.stream())
     for i in range(steps):
-        ctx.head_device(rows, k, n, d_x, k, d_w[i % nbuf], k, d_o, n)
+        launch(i)
     e1.record(ctx.stream())
     e1.synchronize()
     us = e0.elapsed_ms(e1) / steps * 1e3
     nbytes = w_bytes + 4 * rows * k + 4 * rows * n
     gbps = nbytes / (us * 1e-6) / 1e9
-    for a in d_w:
+    for a in d_w + d_q + d_s:
         a.free()
-    return {"workload": f"head {rows}x{k} times bf16 [{n}][{k}], weights from HBM ({nbuf} rotating copies)",
+    fmt = "int8 (+ fp32 scales)" if int8 else "bf16"
+    return {"workload": f"head {rows}x{k} times {fmt} [{n}][{k}], weights from HBM ({nbuf} rotating copies)",
             "us_per_step": round(us, 3), "algorithmic_bytes": nbytes, "hbm_gbps": round(gbps, 1),
             "hbm_pct_peak": round(100 * gbps / HBM_PEAK_GBPS, 2)}
 
@@ -588,8 +602,9 @@ def main() -> int:
                 f"({fb['calls_per_frame']} calls), serial p50 {m['serial_us_p50']} us")
         # logit heads (the step before the sampler): CodecHead and one CodePredictorHead
         for name, (n_rows, n_out) in (("codec_head", (FRAME_ROWS, 3072)), ("codec_head_1", (1, 3072)),
-                                      ("code_predictor_head", (FRAME_ROWS, 2048))):
-            m = measure_head(ctx, n_rows, 1024, n_out, 2000, hip, np)
+                                      ("code_predictor_head", (FRAME_ROWS, 2048)),
+                                      ("codec_head_int8", (FRAME_ROWS, 3072)), ("codec_head_int8_1", (1, 3072))):
+            m = measure_head(ctx, n_rows, 1024, n_out, 2000, hip, np, int8="int8" in name)
             extra[f"{name}_{n_rows}"] = m
             log(f"[bench] {m['workload']}: {m['us_per_step']:.2f} us/step, {m['hbm_gbps']:.0f} GB/s")
         m = measure_device_step(ctx, FRAME_ROWS, 200, hip, np)

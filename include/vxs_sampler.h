@@ -244,6 +244,30 @@ VXS_API int vxs_head_device(vxs_ctx* ctx, int rows, int k, int n, const float* d
                             const uint16_t* d_w, int64_t ldw, float* d_out, int64_t ldo);
 
 /*
+ * The same heads with int8 weights (WeightPrecision.Int8, DecoderStack.cs:7-16; the reference packs
+ * codec_head and every code_predictor.lm_head this way when asked, TalkerModel.cs:37,55):
+ *   out[r][j] = scale[j] * sum_k x[r][k] * q[j][k]
+ * the decode path's form (Gemm.cs:602-680: SmallM, PanelPairDotInt8 / PanelDotInt8, the scale
+ * applied to the fp32 dot). q int8 [n][ldq], scale fp32 [n], as vxs_head_pack_int8_device writes
+ * them. Each entry is within (k + 1) * 2^-24 * scale[j] * sum_k |x q| of the exact value, a bound
+ * the reference's decode form and its batched form (Gemm.cs:95-98, which dequantizes q * scale
+ * first) both satisfy. Needs k <= 2048, k and ldq multiples of 8, ldx a multiple of 4, 16-byte
+ * aligned x and q (else VXS_ERR_UNSUPPORTED). Asynchronous on the context stream.
+ */
+VXS_API int vxs_head_int8_device(vxs_ctx* ctx, int rows, int k, int n, const float* d_x, int64_t ldx,
+                                 const int8_t* d_q, int64_t ldq, const float* d_scale, float* d_out, int64_t ldo);
+
+/*
+ * int8 packing of a bf16 head weight on the GPU, PackedMatrix.FromBf16LinearInt8
+ * (src/Voxwerk/Numerics/PackedMatrix.cs:124-154), bit for bit: per output row j, amax = max_k |W[j][k]|,
+ * scale[j] = amax / 127 (1 when amax is 0), q[j][k] = clamp(round-half-even(W[j][k] * (1 / scale[j])),
+ * -127, 127), in correctly rounded fp32. W bf16 [n][ldw], q int8 [n][ldq], scale fp32 [n]; finite
+ * weights. Asynchronous on the context stream.
+ */
+VXS_API int vxs_head_pack_int8_device(vxs_ctx* ctx, int k, int n, const uint16_t* d_w, int64_t ldw, int8_t* d_q,
+                                      int64_t ldq, float* d_scale);
+
+/*
  * Embedding rows of sampled ids, the step after the sampler, so that ids need not return to the
  * host between sampling and the next forward pass. Tables are bf16 [vocab][hidden], widened to
  * fp32 exactly (Bf16.ToFloat, src/Voxwerk/Numerics/Bf16.cs:13); sums run in the reference's order,

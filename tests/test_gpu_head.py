@@ -1,5 +1,6 @@
-"""GPU: the logit heads (vxs_head_device) through the C ABI against the oracle (oracle/head_np.py),
-and the device-resident step head -> sampler -> embedding.
+"""GPU: the logit heads (vxs_head_device, and the int8 form vxs_head_int8_device with its packing
+vxs_head_pack_int8_device) through the C ABI against the oracle (oracle/head_np.py), and the
+device-resident step head -> sampler -> embedding.
 
 Bar: exact on integer data (every order is exact); within gamma_K * sum|x w| of the exact dot
 product otherwise (the bound the reference's own fp32 order also satisfies); sampled ids on the
@@ -10,7 +11,8 @@ import pytest
 
 from oracle import ref
 from oracle.embedding_np import embed
-from oracle.head_np import head_bound, head_exact
+from oracle.head_np import (head_bound, head_exact, head_int8_batched_fp32, head_int8_bound, head_int8_decode_fp32,
+                            head_int8_exact, pack_int8)
 from voxwerk_amd._lib import PARAMS_DTYPE
 from voxwerk_amd.hip import DeviceArray
 
@@ -102,3 +104,99 @@ def test_step_on_device_head_sampler_embedding(ctx):
     st = embed(ids, emb, want, add=False)
     assert np.array_equal(d_st.numpy(), st)
     assert np.array_equal(d_out.numpy().view(np.uint32), want.view(np.uint32))
+
+
+# ---- int8 weights (WeightPrecision.Int8)
+def _run_int8(ctx, x, q, scale, ldx=None, ldq=None, ldo=None):
+    rows, k = x.shape
+    n = q.shape[0]
+    ldx, ldq, ldo = ldx or k, ldq or k, ldo or n
+    xp = np.zeros((rows, ldx), np.float32)
+    xp[:, :k] = x
+    qp = np.zeros((n, ldq), np.int8)
+    qp[:, :k] = q
+    d_x, d_q, d_s = DeviceArray.from_numpy(xp), DeviceArray.from_numpy(qp), DeviceArray.from_numpy(scale.astype(np.float32))
+    d_o = DeviceArray.from_numpy(np.full((rows, ldo), 7.0, np.float32))
+    print(f"int8 head rows={rows} k={k} n={n} ldx={ldx} ldq={ldq} ldo={ldo}", flush=True)
+    ctx.head_int8_device(rows, k, n, d_x, ldx, d_q, ldq, d_s, d_o, ldo)
+    ctx.synchronize()
+    out = d_o.numpy()
+    assert np.all(out[:, n:] == 7.0)
+    return out[:, :n]
+
+
+def _pack_on_gpu(ctx, w, ldw=None, ldq=None):
+    n, k = w.shape
+    ldw, ldq = ldw or k, ldq or k
+    wp = np.zeros((n, ldw), np.uint16)
+    wp[:, :k] = w
+    d_w = DeviceArray.from_numpy(wp)
+    d_q = DeviceArray.from_numpy(np.full((n, ldq), 99, np.int8))
+    d_s = DeviceArray((n,), np.float32)
+    print(f"int8 pack n={n} k={k} ldw={ldw} ldq={ldq}", flush=True)
+    ctx.head_pack_int8_device(k, n, d_w, ldw, d_q, ldq, d_s)
+    ctx.synchronize()
+    qv = d_q.numpy()
+    assert np.all(qv[:, k:] == 99)
+    return qv[:, :k], d_s.numpy()
+
+
+@pytest.mark.parametrize("n,k,ldw,ldq", [(3072, 1024, 1024, 1024), (2048, 1024, 1032, 1040), (7, 300, 301, 300),
+                                         (1, 2048, 2048, 2048)])
+def test_pack_int8_bit_exact(ctx, n, k, ldw, ldq):
+    rng = np.random.default_rng(n + k)
+    wf = rng.standard_normal((n, k)) * np.exp(rng.uniform(-8, 3, (n, 1)))
+    if n >= 4:
+        wf[0] = 0.0  # all-zero row: scale 1
+        wf[1, :8] = [127.0, -63.5, 2.5, 3.5, -0.5, 0.0, 1.5, -126.5]  # ties at scale 1
+        wf[1, 8:] = np.clip(wf[1, 8:], -100, 100)
+        wf[2] = np.round(wf[2] * 4) / 4
+    w = _bf16(wf)
+    q, scale = _pack_on_gpu(ctx, w, ldw, ldq)
+    wq, ws = pack_int8(w)
+    assert np.array_equal(scale.view(np.uint32), ws.view(np.uint32))
+    assert np.array_equal(q, wq)
+
+
+@pytest.mark.parametrize("rows,k,n,scale", [(1, 1024, 3072, 1.0), (24, 1024, 2048, 0.5), (5, 1024, 3001, 0.25),
+                                            (3, 2048, 100, 1.0)])
+def test_head_int8_exact_on_integers(ctx, rows, k, n, scale):
+    """Small integers and a power-of-two scale: every partial sum and the scaling are exact."""
+    rng = np.random.default_rng(rows * 7 + n)
+    x = rng.integers(-8, 9, (rows, k)).astype(np.float32)
+    q = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    sc = np.full(n, scale, np.float32)
+    got = _run_int8(ctx, x, q, sc)
+    want = (x.astype(np.int64) @ q.astype(np.int64).T).astype(np.float64) * scale
+    assert np.array_equal(got.astype(np.float64), want)
+
+
+@pytest.mark.parametrize("rows,k,n,pad", [(24, 1024, 3072, 0), (1, 1024, 2048, 0), (64, 1024, 3072, 8),
+                                          (3, 200, 100, 0), (7, 776, 1000, 16), (9, 1536, 513, 0),
+                                          (2, 2048, 3072, 0), (4, 8, 7, 0), (1, 1536, 3001, 8)])
+def test_head_int8_within_bound(ctx, rows, k, n, pad):
+    """Weights packed on the GPU, then the head: within gamma_{K+1} * scale * sum|x q| of the exact
+    value, the bound both reference forms (decode and batched) satisfy."""
+    rng = np.random.default_rng(rows * 1000 + k + n + 1)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    w = _bf16(rng.standard_normal((n, k)) * 0.05)
+    q, scale = _pack_on_gpu(ctx, w, ldw=k + pad, ldq=k + pad)
+    got = _run_int8(ctx, x, q, scale, ldx=k + pad, ldq=k + pad, ldo=n + pad)
+    exact, bound = head_int8_exact(x, q, scale), head_int8_bound(x, q, scale)
+    err = np.abs(got - exact)
+    assert np.all(err <= bound), f"max err/bound {np.max(err / bound):.3f}"
+    if rows * n * k <= 2_000_000:  # the reference's own two fp32 forms on the same packed weight
+        for ref_form in (head_int8_decode_fp32, head_int8_batched_fp32):
+            assert np.all(np.abs(ref_form(x, q, scale).astype(np.float64) - exact) <= bound)
+
+
+def test_head_int8_rejects_unsupported_shapes(ctx):
+    from voxwerk_amd.sampler import SamplerError
+
+    d = DeviceArray((4, 4096), np.float32)
+    q = DeviceArray((4, 4096), np.int8)
+    s = DeviceArray((4,), np.float32)
+    o = DeviceArray((4, 4), np.float32)
+    for k, ldx, ldq in ((2056, 2056, 2056), (12, 12, 12), (16, 18, 16), (16, 16, 20)):
+        with pytest.raises(SamplerError):
+            ctx.head_int8_device(1, k, 4, d, ldx, q, ldq, s, o, 4)

@@ -466,3 +466,67 @@ def test_head_bound_holds_for_fp32_sums_in_two_orders():
             for got in (float(seq), float(pair[0])):
                 assert abs(got - exact[r, n]) <= bound[r, n], (r, n)
     assert np.all(bound > 0) and np.all(bound < 1e-3 * np.abs(x).sum() * 4)
+
+
+def test_pack_int8_hand_derived_rows():
+    """FromBf16LinearInt8 on rows whose scale is exact: ties go to even, the extreme maps to 127."""
+    from oracle.head_np import pack_int8
+
+    w = _bf16(np.array([[127.0, -63.5, 2.5, 3.5, -0.5, 0.0, 1.5, -126.5],  # amax 127: scale 1
+                        [254.0, 3.0, 5.0, -254.0, 1.0, -3.0, 0.0, 7.0],  # amax 254: scale 2, w/2
+                        [0.0] * 8,  # all zero: scale 1, q 0
+                        [-0.25, 0.125, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0]], np.float32))  # amax 1/4
+    q, scale = pack_int8(w)
+    assert scale.tolist()[:3] == [1.0, 2.0, 1.0]
+    assert q[0].tolist() == [127, -64, 2, 4, 0, 0, 2, -126]
+    assert q[1].tolist() == [127, 2, 2, -127, 0, -2, 0, 4]
+    assert q[2].tolist() == [0] * 8
+    assert scale[3] == np.float32(0.25) / np.float32(127.0) and q[3].tolist()[:2] == [-127, 64]
+
+
+def test_pack_int8_against_python_floats():
+    """Per element in Python: the fp32 quotient and product as the correctly rounded value of the
+    exact rational (fractions), round-half-even by Python's round(); differently computed."""
+    from fractions import Fraction
+
+    from oracle.embedding_np import widen
+    from oracle.head_np import pack_int8
+
+    rng = np.random.default_rng(5)
+    w = _bf16(rng.standard_normal((12, 64)) * np.exp(rng.uniform(-6, 6, (12, 1))))
+    q, scale = pack_int8(w)
+    wf = widen(w)
+
+    def f32(fr):  # nearest fp32 to a rational (fp32-normal range): exact via scaling
+        e = int(np.floor(np.log2(abs(float(fr))))) if fr != 0 else 0
+        m = fr / Fraction(2) ** (e - 23)
+        n = round(m)  # ties to even
+        return float(Fraction(n) * Fraction(2) ** (e - 23))
+
+    for r in range(12):
+        amax = max(abs(Fraction(float(v))) for v in wf[r])
+        s = f32(amax / 127) if amax > 0 else 1.0
+        inv = f32(1 / Fraction(s))
+        assert float(scale[r]) == s
+        for c in range(64):
+            p = f32(Fraction(float(wf[r, c])) * Fraction(inv)) if wf[r, c] != 0 else 0.0
+            assert int(q[r, c]) == max(-127, min(127, round(p))), (r, c)
+
+
+def test_head_int8_bound_holds_for_both_reference_forms():
+    from oracle.head_np import (head_int8_batched_fp32, head_int8_bound, head_int8_decode_fp32, head_int8_exact,
+                                pack_int8)
+
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((3, 256)).astype(np.float32)
+    q, scale = pack_int8(_bf16(rng.standard_normal((20, 256)) * 0.05))
+    exact, bound = head_int8_exact(x, q, scale), head_int8_bound(x, q, scale)
+    for got in (head_int8_decode_fp32(x, q, scale), head_int8_batched_fp32(x, q, scale)):
+        assert np.all(np.abs(got.astype(np.float64) - exact) <= bound)
+    # integers with a power-of-two scale: exact in every order
+    xi = rng.integers(-8, 9, (2, 256)).astype(np.float32)
+    qi = rng.integers(-127, 128, (5, 256)).astype(np.int8)
+    si = np.full(5, 0.5, np.float32)
+    want = (xi.astype(np.int64) @ qi.astype(np.int64).T) * 0.5
+    assert np.array_equal(head_int8_exact(xi, qi, si), want)
+    assert np.array_equal(head_int8_decode_fp32(xi, qi, si).astype(np.float64), want)

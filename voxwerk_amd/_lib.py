@@ -103,6 +103,8 @@ _SIGNATURES = {
     "vxs_history_seed": (c_int, [c_void_p, c_void_p, c_int, c_int32]),
     "vxs_embed_device": (c_int, [c_void_p, c_int, c_int, _P, _P, c_int, _P, c_int64, c_int, _P]),
     "vxs_head_device": (c_int, [c_void_p, c_int, c_int, c_int, _P, c_int64, _P, c_int64, _P, c_int64]),
+    "vxs_head_int8_device": (c_int, [c_void_p, c_int, c_int, c_int, _P, c_int64, _P, c_int64, _P, _P, c_int64]),
+    "vxs_head_pack_int8_device": (c_int, [c_void_p, c_int, c_int, _P, c_int64, _P, c_int64, _P]),
     "vxs_frame_embed_device": (c_int, [c_void_p, c_int, c_int, c_int, _P, c_int64, c_int64, _P, c_int, _P, c_int, _P,
                                        c_int64, _P, c_int64, _P]),
     "vxs_history_draw": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, _P]),

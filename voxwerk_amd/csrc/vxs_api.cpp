@@ -1131,8 +1131,44 @@ VXS_API int vxs_head_device(vxs_ctx* ctx, int rows, int k, int n, const float* d
         if (rows == 0) return VXS_OK;
         if (!d_x || !d_w || !d_out) return fail(ctx, VXS_ERR_INVALID_ARG, "null pointer");
         VXS_HIP(ctx, hipSetDevice(ctx->device));
-        vxs::HeadArgs a{rows, k, n, d_x, ldx, d_w, ldw, d_out, ldo};
+        vxs::HeadArgs a{rows, k, n, d_x, ldx, d_w, ldw, d_out, ldo, 0, nullptr, nullptr};
         VXS_HIP(ctx, vxs::launch_head(a, ctx->stream));
+        ctx->err.clear();
+        return VXS_OK;
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
+VXS_API int vxs_head_int8_device(vxs_ctx* ctx, int rows, int k, int n, const float* d_x, int64_t ldx, const int8_t* d_q,
+                                 int64_t ldq, const float* d_scale, float* d_out, int64_t ldo) {
+    try {
+        if (!ctx) return VXS_ERR_INVALID_ARG;
+        if (rows < 0 || k <= 0 || n <= 0 || ldx < k || ldq < k || ldo < n)
+            return fail(ctx, VXS_ERR_INVALID_ARG, "bad rows, k, n or leading dimensions");
+        if (k > 2048 || k % 8 != 0 || ldq % 8 != 0 || ldx % 4 != 0 || ((uintptr_t)d_x & 15u) || ((uintptr_t)d_q & 15u))
+            return fail(ctx, VXS_ERR_UNSUPPORTED,
+                        "int8 head needs k <= 2048, k and ldq multiples of 8, ldx a multiple of 4, 16-byte aligned x and q");
+        if (rows == 0) return VXS_OK;
+        if (!d_x || !d_q || !d_scale || !d_out) return fail(ctx, VXS_ERR_INVALID_ARG, "null pointer");
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        vxs::HeadArgs a{rows, k, n, d_x, ldx, nullptr, ldq, d_out, ldo, 0, d_q, d_scale};
+        VXS_HIP(ctx, vxs::launch_head(a, ctx->stream));
+        ctx->err.clear();
+        return VXS_OK;
+    } catch (...) {
+        return fail(ctx, VXS_ERR_INVALID_ARG, "unknown exception");
+    }
+}
+
+VXS_API int vxs_head_pack_int8_device(vxs_ctx* ctx, int k, int n, const uint16_t* d_w, int64_t ldw, int8_t* d_q,
+                                      int64_t ldq, float* d_scale) {
+    try {
+        if (!ctx) return VXS_ERR_INVALID_ARG;
+        if (k <= 0 || n <= 0 || ldw < k || ldq < k) return fail(ctx, VXS_ERR_INVALID_ARG, "bad k, n or leading dimensions");
+        if (!d_w || !d_q || !d_scale) return fail(ctx, VXS_ERR_INVALID_ARG, "null pointer");
+        VXS_HIP(ctx, hipSetDevice(ctx->device));
+        VXS_HIP(ctx, vxs::launch_head_pack_int8(k, n, d_w, ldw, d_q, ldq, d_scale, ctx->stream));
         ctx->err.clear();
         return VXS_OK;
     } catch (...) {

@@ -15,6 +15,15 @@
 // partner's other half) and then plain butterflies (xor 4, 2, 1): with R = 8, lane l ends with
 // output 4 b5 + 2 b4 + b3 of the wave, summed over all 64 lanes. The fp32 sum order is this kernel's own;
 // it differs from the reference's AVX-512 order by rounding only (bounded by K 2^-24 sum |x w|).
+//
+// The int8 form (WeightPrecision.Int8, DecoderStack.cs:7-16) keeps W as q[n][k] in [-127, 127] and
+// one fp32 scale per output (PackedMatrix.FromBf16LinearInt8, PackedMatrix.cs:124-154):
+// out[r][n] = scale[n] * sum_k x[r][k] * q[n][k], the scale applied to the fp32 dot as the decode
+// path does (Gemm.cs:650-680, PanelPairDotInt8 / PanelDotInt8). Same layout and reduction, half the
+// weight bytes; a lane widens its int8 slice to fp32 once (exact) and keeps it in registers for
+// every row, so a row costs one FMA per weight. The packing itself runs on the GPU too
+// (head_pack_i8_kernel): per output the largest |w|, scale = amax / 127 (1 for an all-zero row),
+// q = clamp(round-half-even(w * (1 / scale)), -127, 127), all in correctly rounded fp32.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -81,6 +90,32 @@ __device__ __forceinline__ void halve(const float (&in)[2 * H], float (&out)[H],
     }
 }
 
+// The wave's R partial dots of one row reduced to one output per lane group (see the layout note).
+template <int R>
+__device__ __forceinline__ float reduce_outputs(const float (&v)[R], int lane) {
+    constexpr int kGroup = 64 / R;
+    float sum;
+    if constexpr (R == 8) {
+        float q[4], t[2], s1[1];
+        halve<4>(v, q, lane, 32);
+        halve<2>(q, t, lane, 16);
+        halve<1>(t, s1, lane, 8);
+        sum = s1[0];
+    } else if constexpr (R == 4) {
+        float q[2], s1[1];
+        halve<2>(v, q, lane, 32);
+        halve<1>(q, s1, lane, 16);
+        sum = s1[0];
+    } else {
+        float s1[1];
+        halve<1>(v, s1, lane, 32);
+        sum = s1[0];
+    }
+#pragma unroll
+    for (int mask = kGroup / 2; mask >= 1; mask /= 2) sum += __shfl_xor(sum, mask);
+    return sum;
+}
+
 // R outputs per wave (8 or 4), KJ slices of 8 per lane (k <= 512 KJ).
 template <int KJ, int R, bool FULL>
 __global__ __launch_bounds__(kHT) void head_kernel(HeadArgs a) {
@@ -125,25 +160,7 @@ __global__ __launch_bounds__(kHT) void head_kernel(HeadArgs a) {
             for (int j = 0; j < KJ; j++) acc = dot8(w[o][j], x.a[j], x.b[j], acc);
             v[o] = acc;
         }
-        float sum;
-        if constexpr (R == 8) {
-            float q[4], t[2], s1[1];
-            halve<4>(v, q, lane, 32);
-            halve<2>(q, t, lane, 16);
-            halve<1>(t, s1, lane, 8);
-            sum = s1[0];
-        } else if constexpr (R == 4) {
-            float q[2], s1[1];
-            halve<2>(v, q, lane, 32);
-            halve<1>(q, s1, lane, 16);
-            sum = s1[0];
-        } else {
-            float s1[1];
-            halve<1>(v, s1, lane, 32);
-            sum = s1[0];
-        }
-#pragma unroll
-        for (int mask = kGroup / 2; mask >= 1; mask /= 2) sum += __shfl_xor(sum, mask);
+        const float sum = reduce_outputs<R>(v, lane);
         if ((lane & (kGroup - 1)) == 0 && n0 + o_mine < a.n) a.out[(int64_t)m * a.ldo + n0 + o_mine] = sum;
     };
     // this workgroup's rows: group blockIdx.y of a.row_group rows
@@ -159,6 +176,100 @@ __global__ __launch_bounds__(kHT) void head_kernel(HeadArgs a) {
     }
 }
 
+typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+
+// int8 weights, widened once: R outputs per wave, KJ slices of 8 per lane (k <= 512 KJ).
+template <int KJ, int R, bool FULL>
+__global__ __launch_bounds__(kHT) void head_i8_kernel(HeadArgs a) {
+    static_assert(R == 8 || R == 4 || R == 2, "eight, four or two outputs per wave");
+    constexpr int kGroup = 64 / R;
+    const int lane = threadIdx.x & 63;
+    const int n0 = (blockIdx.x * (kHT / 64) + (threadIdx.x >> 6)) * R;
+    if (n0 >= a.n) return;  // whole wave past the last output (wave-uniform)
+
+    // every lane loads from inside q (a clamped address) and zeroes what lies outside; all loads
+    // are issued before the first conversion
+    u2 raw[R][KJ];
+#pragma unroll
+    for (int o = 0; o < R; o++)
+#pragma unroll
+        for (int j = 0; j < KJ; j++) {
+            const int k = 512 * j + 8 * lane;
+            const int8_t* p = a.q + (int64_t)min(n0 + o, a.n - 1) * a.ldw + (FULL || k < a.k ? k : 0);
+            raw[o][j] = __builtin_nontemporal_load(reinterpret_cast<const u2*>(p));
+        }
+    // q = (q + 128) - 128: the biased byte (sign bit flipped) converted as unsigned, then an exact
+    // fp32 subtraction. (A sign-extended byte fed straight to the conversion was compiled here into
+    // an unsigned conversion of the extended value.)
+    float w[R][KJ][8];
+#pragma unroll
+    for (int o = 0; o < R; o++)
+#pragma unroll
+        for (int j = 0; j < KJ; j++) {
+            const int k = 512 * j + 8 * lane;
+            const bool in = n0 + o < a.n && (FULL || k < a.k);
+            const uint32_t lo = raw[o][j].x ^ 0x80808080u, hi = raw[o][j].y ^ 0x80808080u;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float f = (float)(((i < 4 ? lo : hi) >> (8 * (i & 3))) & 0xffu) - 128.0f;
+                w[o][j][i] = in ? f : 0.0f;
+            }
+        }
+    const int o_mine = R == 8   ? 4 * ((lane >> 5) & 1) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1)
+                       : R == 4 ? 2 * ((lane >> 5) & 1) + ((lane >> 4) & 1)
+                                : (lane >> 5) & 1;
+    const float sc = a.scale[min(n0 + o_mine, a.n - 1)];
+    auto row = [&](int m, const XSlice<KJ>& x) {
+        float v[R];
+#pragma unroll
+        for (int o = 0; o < R; o++) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < KJ; j++) {
+                const float xs[8] = {x.a[j].x, x.a[j].y, x.a[j].z, x.a[j].w, x.b[j].x, x.b[j].y, x.b[j].z, x.b[j].w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc = __builtin_fmaf(w[o][j][i], xs[i], acc);
+            }
+            v[o] = acc;
+        }
+        const float sum = reduce_outputs<R>(v, lane) * sc;
+        if ((lane & (kGroup - 1)) == 0 && n0 + o_mine < a.n) a.out[(int64_t)m * a.ldo + n0 + o_mine] = sum;
+    };
+    const int first = blockIdx.y * a.row_group;
+    const int last = min(a.rows, first + a.row_group) - 1;
+    XSlice<KJ> x0 = load_x<KJ, FULL>(a, first, lane);
+    for (int m = first; m <= last; m += 2) {
+        XSlice<KJ> x1 = load_x<KJ, FULL>(a, min(m + 1, last), lane);
+        row(m, x0);
+        if (m + 1 > last) break;
+        x0 = load_x<KJ, FULL>(a, min(m + 2, last), lane);
+        row(m + 1, x1);
+    }
+}
+
+// FromBf16LinearInt8 for one output row per workgroup.
+__global__ __launch_bounds__(kHT) void head_pack_i8_kernel(int k, const uint16_t* __restrict__ w, int64_t ldw,
+                                                          int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale) {
+    __shared__ float wmax[kHT / 64];
+    const int n = blockIdx.x;
+    const uint16_t* row = w + (int64_t)n * ldw;
+    float amax = 0.0f;
+    for (int i = threadIdx.x; i < k; i += kHT) amax = fmaxf(amax, fabsf(__uint_as_float((uint32_t)row[i] << 16)));
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask /= 2) amax = fmaxf(amax, __shfl_xor(amax, mask));
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float scl = amax > 0.0f ? amax / 127.0f : 1.0f;  // correctly rounded fp32 divisions
+    const float inv = 1.0f / scl;
+    int8_t* qr = q + (int64_t)n * ldq;
+    for (int i = threadIdx.x; i < k; i += kHT) {
+        const float t = rintf(__uint_as_float((uint32_t)row[i] << 16) * inv);  // half to even, as MathF.Round
+        qr[i] = (int8_t)min(max((int)t, -127), 127);
+    }
+    if (threadIdx.x == 0) scale[n] = scl;
+}
+
 // Rows are split into groups, one grid row each, so that the launch has about 2048 waves for the
 // chip's 1024 SIMDs; a group keeps at least two rows (the loads of one overlap the other's work).
 // Every group reads the weight again, from the last-level cache after the first.
@@ -169,10 +280,16 @@ hipError_t launch_kr(HeadArgs a, hipStream_t stream) {
     const int groups = std::max(1, std::min(2048 / waves, a.rows / 2));
     a.row_group = (a.rows + groups - 1) / groups;
     const dim3 grid(tiles, (a.rows + a.row_group - 1) / a.row_group);
-    if (a.k == 512 * KJ)
+    if (a.q) {
+        if (a.k == 512 * KJ)
+            hipLaunchKernelGGL((head_i8_kernel<KJ, R, true>), grid, dim3(kHT), 0, stream, a);
+        else
+            hipLaunchKernelGGL((head_i8_kernel<KJ, R, false>), grid, dim3(kHT), 0, stream, a);
+    } else if (a.k == 512 * KJ) {
         hipLaunchKernelGGL((head_kernel<KJ, R, true>), grid, dim3(kHT), 0, stream, a);
-    else
+    } else {
         hipLaunchKernelGGL((head_kernel<KJ, R, false>), grid, dim3(kHT), 0, stream, a);
+    }
     return hipGetLastError();
 }
 
@@ -190,6 +307,13 @@ hipError_t launch_head(const HeadArgs& a, hipStream_t stream) {
         case 4: return few ? launch_kr<4, 2>(a, stream) : launch_kr<4, 4>(a, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_head_pack_int8(int k, int n, const uint16_t* w, int64_t ldw, int8_t* q, int64_t ldq, float* scale,
+                                 hipStream_t stream) {
+    if (n <= 0 || k <= 0) return hipSuccess;
+    hipLaunchKernelGGL(head_pack_i8_kernel, dim3(n), dim3(kHT), 0, stream, k, w, ldw, q, ldq, scale);
+    return hipGetLastError();
 }
 
 }  // namespace vxs

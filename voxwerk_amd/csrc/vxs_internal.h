@@ -203,13 +203,18 @@ struct HeadArgs {
     int rows, k, n;
     const float* x;
     int64_t ldx;
-    const uint16_t* w;
-    int64_t ldw;
+    const uint16_t* w;    // bf16 weight [n][ldw], or null for the int8 form
+    int64_t ldw;          // leading dimension of w or q, in elements
     float* out;
     int64_t ldo;
-    int row_group;  // rows per workgroup (set by the launcher)
+    int row_group;        // rows per workgroup (set by the launcher)
+    const int8_t* q;      // int8 weight [n][ldw] (WeightPrecision.Int8), or null
+    const float* scale;   // its per-output scale [n]
 };
 hipError_t launch_head(const HeadArgs& a, hipStream_t stream);
+// int8 packing of a bf16 weight: q[n][ldq], scale[n] (PackedMatrix.FromBf16LinearInt8).
+hipError_t launch_head_pack_int8(int k, int n, const uint16_t* w, int64_t ldw, int8_t* q, int64_t ldq, float* scale,
+                                 hipStream_t stream);
 hipError_t launch_frame_embed(const FrameEmbedArgs& a, hipStream_t stream);
 
 // Fixed device scratch of vxs_sample_noalloc (vxs_noalloc.hip): its size, and its device address on

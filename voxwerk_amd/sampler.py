@@ -383,6 +383,14 @@ class Context:
         """vxs_head_device: out[r][j] = sum_k x[r][k] * W[j][k] (CodecHead / CodePredictorHead)."""
         self._check(self._lib.vxs_head_device(self._h, rows, k, n, ptr(x), ldx, ptr(w), ldw, ptr(out), ldo))
 
+    def head_int8_device(self, rows: int, k: int, n: int, x, ldx: int, q, ldq: int, scale, out, ldo: int) -> None:
+        """vxs_head_int8_device: out[r][j] = scale[j] * sum_k x[r][k] * q[j][k] (WeightPrecision.Int8)."""
+        self._check(self._lib.vxs_head_int8_device(self._h, rows, k, n, ptr(x), ldx, ptr(q), ldq, ptr(scale), ptr(out), ldo))
+
+    def head_pack_int8_device(self, k: int, n: int, w, ldw: int, q, ldq: int, scale) -> None:
+        """vxs_head_pack_int8_device: PackedMatrix.FromBf16LinearInt8 of a bf16 [n][ldw] weight."""
+        self._check(self._lib.vxs_head_pack_int8_device(self._h, k, n, ptr(w), ldw, ptr(q), ldq, ptr(scale)))
+
     def embed_device(self, rows: int, hidden: int, ids, table, vocab: int, out, ld_out: int, add: bool, status) -> None:
         """vxs_embed_device: out[r] = table[ids[r]] or += it (CodecEmbedding / CodePredictorEmbedding)."""
         self._check(self._lib.vxs_embed_device(self._h, rows, hidden, ptr(ids), ptr(table), vocab, ptr(out), ld_out,
