@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from talker_model import OracleContext, SyntheticTalker
-from voxwerk_amd.generate import BatchJob, generate, generate_batch
+from voxwerk_amd.generate import BatchJob, CancellationToken, OperationCanceledError, generate, generate_batch
 from voxwerk_amd.sampler import CODEC_EOS_ID, GenerationOptions, SamplingOptions
 
 
@@ -65,3 +65,53 @@ def test_generate_batch_rejects_bad_batch():
     with pytest.raises(ValueError):
         generate_batch(_jobs(), 0, lambda j, f: None, SyntheticTalker(), context=OracleContext())
     generate_batch([], 4, lambda j, f: None, SyntheticTalker(), context=OracleContext())
+
+
+def test_generate_on_frame_counts_frames():
+    """onFrame(frames.Count) after every frame (TalkerGenerator.cs:277)."""
+    ctx, model = OracleContext(), SyntheticTalker(seed=5)
+    seen = []
+    frames = generate(0, _jobs()[0].Options, model, context=ctx, on_frame=seen.append)
+    assert seen == list(range(1, len(frames) + 1))
+
+
+def test_generate_cancellation_stops_at_the_next_step():
+    """ct.ThrowIfCancellationRequested() at the top of each step (TalkerGenerator.cs:243): cancelling from
+    the frame callback ends the loop before the next talker Select."""
+    ctx, model = OracleContext(), SyntheticTalker(seed=5)
+    opts = _jobs()[0].Options
+    full = generate(0, opts, model, context=ctx)
+    assert len(full) >= 3
+    ct = CancellationToken()
+    seen = []
+
+    def on_frame(n):
+        seen.append(n)
+        if n == 2:
+            ct.cancel()
+
+    with pytest.raises(OperationCanceledError):
+        generate(0, opts, SyntheticTalker(seed=5), context=ctx, ct=ct, on_frame=on_frame)
+    assert seen == [1, 2]
+    with pytest.raises(OperationCanceledError):  # already cancelled: no step runs
+        generate(0, opts, model, context=ctx, ct=ct)
+
+
+def test_generate_batch_cancellation():
+    """GenerateBatch checks the token once per step (TalkerGenerator.cs:332): jobs reported before the
+    cancel keep their frames, the rest are never reported."""
+    ctx, model = OracleContext(), SyntheticTalker(seed=1)
+    jobs = _jobs()
+    full = _run_batch(ctx, jobs, 2, model)
+    ct = CancellationToken()
+    done = {}
+
+    def on_done(job, frames):
+        done[job] = [f.copy() for f in frames]
+        ct.cancel()
+
+    with pytest.raises(OperationCanceledError):
+        generate_batch(jobs, 2, on_done, SyntheticTalker(seed=1), context=ctx, ct=ct)
+    assert len(done) >= 1 and len(done) < len(jobs)
+    for j, frames in done.items():
+        assert all(np.array_equal(a, b) for a, b in zip(frames, full[j])) and len(frames) == len(full[j])

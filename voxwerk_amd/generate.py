@@ -22,6 +22,30 @@ from .sampler import (CODEC_EOS_ID, CP_VOCAB, TALKER_VOCAB, Context, GenerationO
 NUM_CODE_GROUPS = 16  # Qwen3TtsConfig.NumCodeGroups: codebook 0 from the talker, 1..15 from the code predictor
 
 
+class OperationCanceledError(Exception):
+    """Raised when a generation loop sees its token cancelled (.NET's OperationCanceledException)."""
+
+
+class CancellationToken:
+    """The ``CancellationToken`` the reference's loops take (TalkerGenerator.cs:213, :323): a flag set
+    from any thread by ``cancel()``, checked once per step. Cancellation leaves the context and the
+    library usable; a batch releases its resident history store on the way out."""
+
+    def __init__(self) -> None:
+        self._cancelled = False
+
+    def cancel(self) -> None:
+        self._cancelled = True
+
+    @property
+    def is_cancellation_requested(self) -> bool:
+        return self._cancelled
+
+    def throw_if_cancellation_requested(self) -> None:
+        if self._cancelled:
+            raise OperationCanceledError("generation cancelled")
+
+
 class TalkerModel(Protocol):
     """The model side of generation. ``job`` identifies a sequence (its prompt and its caches).
 
@@ -67,10 +91,12 @@ def _sub_seed(opts: GenerationOptions) -> Optional[int]:
 
 
 def generate(job: int, opts: GenerationOptions, model: TalkerModel, context: Optional[Context] = None,
-             vocab: int = TALKER_VOCAB, groups: int = NUM_CODE_GROUPS, eos_id: int = CODEC_EOS_ID) -> List[np.ndarray]:
+             vocab: int = TALKER_VOCAB, groups: int = NUM_CODE_GROUPS, eos_id: int = CODEC_EOS_ID,
+             ct: Optional[CancellationToken] = None, on_frame: Optional[Callable[[int], None]] = None) -> List[np.ndarray]:
     """One sequence, step by step as ``Generate`` (TalkerGenerator.cs:213-287): penalty, suppression
     and ``Select`` on the talker row, then ``groups - 1`` code-predictor ``Select`` calls. Returns the
-    frames, each ``groups`` codes."""
+    frames, each ``groups`` codes. ``ct`` is checked at the start of every step (:243) and raises
+    ``OperationCanceledError``; ``on_frame(n)`` is called with the frame count after each frame (:277)."""
     ctx = context or default_context()
     sampler = Sampler(opts.Seed, ctx)
     sub_sampler = Sampler(_sub_seed(opts), ctx)
@@ -78,6 +104,8 @@ def generate(job: int, opts: GenerationOptions, model: TalkerModel, context: Opt
     history: List[int] = []
     frames: List[np.ndarray] = []
     for t in range(opts.MaxNewTokens):
+        if ct is not None:
+            ct.throw_if_cancellation_requested()                                               # :243
         lg = np.ascontiguousarray(logits[:vocab], dtype=np.float32)
         Sampler.ApplyRepetitionPenalty(lg, history, opts.RepetitionPenalty, context=ctx)      # :246
         keep = lg[eos_id]
@@ -95,6 +123,8 @@ def generate(job: int, opts: GenerationOptions, model: TalkerModel, context: Opt
             cp = np.array(model.code_predictor([job], g, frame[None, :]), dtype=np.float32).reshape(-1)
             frame[g] = sub_sampler.Select(cp, opts.SubTalker)
         frames.append(frame)
+        if on_frame is not None:
+            on_frame(len(frames))                                                              # :277
         logits = np.array(model.talker_step([job], [t], frame[None, :]), dtype=np.float32).reshape(-1)
     return frames
 
@@ -102,7 +132,7 @@ def generate(job: int, opts: GenerationOptions, model: TalkerModel, context: Opt
 def generate_batch(jobs: Sequence[BatchJob], max_batch: int, on_done: Callable[[int, List[np.ndarray]], None],
                    model: TalkerModel, context: Optional[Context] = None, vocab: int = TALKER_VOCAB,
                    cp_vocab: int = CP_VOCAB, groups: int = NUM_CODE_GROUPS, eos_id: int = CODEC_EOS_ID,
-                   path: str = "auto", device_rng: bool = False) -> None:
+                   path: str = "auto", device_rng: bool = False, ct: Optional[CancellationToken] = None) -> None:
     """``GenerateBatch`` (TalkerGenerator.cs:322-455): up to ``max_batch`` sequences advance in
     lockstep; a finished one is reported through ``on_done(job, frames)`` and its slot refilled from the
     queue. Each job keeps its own ``Sampler(Seed)`` / ``Sampler(Seed + 1)``, so its frames do not
@@ -111,7 +141,9 @@ def generate_batch(jobs: Sequence[BatchJob], max_batch: int, on_done: Callable[[
     Per step: one ``vxs_sample_batch`` over the talker rows (penalty from the resident history,
     suppression, select, on-device ``History.Add``), then one per code-predictor group. With
     ``device_rng`` the two generators of each job live in its slot and draw on the GPU (the same
-    .NET sequences, so the same frames); otherwise the host draws them."""
+    .NET sequences, so the same frames); otherwise the host draws them. ``ct`` is checked at the
+    start of every step (:332) and raises ``OperationCanceledError``; jobs already reported stay
+    reported, the rest are dropped, and the resident history store is released."""
     if max_batch <= 0:
         raise ValueError("max_batch must be positive")
     ctx = context or default_context()
@@ -124,6 +156,8 @@ def generate_batch(jobs: Sequence[BatchJob], max_batch: int, on_done: Callable[[
     nxt = 0
     try:
         while nxt < len(jobs) or active:
+            if ct is not None:
+                ct.throw_if_cancellation_requested()                                           # :332
             while len(active) < max_batch and nxt < len(jobs):                                 # :334-360
                 opts = jobs[nxt].Options
                 slot = free.pop()
