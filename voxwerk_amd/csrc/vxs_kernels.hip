@@ -1411,18 +1411,17 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void sa
     const int lane = threadIdx.x & 63;
     const int r0 = blockIdx.x * kWaves;
     const int r = r0 + wv;
-    // Staggered rounds: workgroups reach the CUs in index order, about 256 per round (one per CU),
-    // and a 4096-row batch puts four rounds on every CU, one wave of each per SIMD. A later round
-    // starts its loads about 1.7 us (2 x 2048 cycles of s_sleep) after the one before and runs at
-    // a lower wave priority, so the earlier rows arrive first and compute while the later ones
-    // load (4096 x 3072: 22.0 -> 21.3 us; priority alone 21.7 us; a 2.6 us stagger 22.4 us; the
-    // round taken from the wave's slot on its SIMD instead of the workgroup index: the same).
+    // Staggered halves: workgroups reach the CUs in index order, about 256 per round (one per CU),
+    // and a 4096-row batch puts four rounds on every CU, one wave of each per SIMD. The second
+    // half of the batch (two waves per SIMD) starts its loads about 2.6 us (3 x 2048 cycles of
+    // s_sleep) after the first and runs at a lower wave priority, so the first half's rows arrive
+    // first and compute, two waves per SIMD, while the second half loads. 4096 x 3072: 22.0 ->
+    // 21.0 us. Tried: priority alone 21.7 us; four rounds 1.7 us apart 21.3 us (2.6 us apart 22.4);
+    // rounds from the wave's slot on its SIMD instead of the workgroup index: the same.
     {
-        const uint32_t round = blockIdx.x >> 8;
-        if (round == 0) __builtin_amdgcn_s_setprio(3);
-        else if (round == 1) __builtin_amdgcn_s_setprio(2);
-        else if (round == 2) __builtin_amdgcn_s_setprio(1);
-                for (uint32_t i = 0; i < 2u * min(round, 3u); i++) __builtin_amdgcn_s_sleep(32);
+        const uint32_t half = blockIdx.x >> 9;
+        if (half == 0) __builtin_amdgcn_s_setprio(3);
+        for (uint32_t i = 0; i < 3u * min(half, 1u); i++) __builtin_amdgcn_s_sleep(32);
     }
     int b = 0;
     if (r < a.rows) b = wave_fast_row<NS, kStats>(a, vec, r, lane, sm.wave[wv]);
