@@ -200,3 +200,28 @@ def test_head_int8_rejects_unsupported_shapes(ctx):
     for k, ldx, ldq in ((2056, 2056, 2056), (12, 12, 12), (16, 18, 16), (16, 16, 20)):
         with pytest.raises(SamplerError):
             ctx.head_int8_device(1, k, 4, d, ldx, q, ldq, s, o, 4)
+
+
+def test_step_on_device_int8_head_sampler(ctx):
+    """Hidden rows -> int8 CodecHead (weights packed on the GPU) -> sampler, the logits never leaving
+    the GPU (WeightPrecision.Int8): logits within the int8 bound, ids equal to the oracle's on them."""
+    rng = np.random.default_rng(43)
+    rows, hidden, vocab = 24, 1024, 3072
+    x = rng.standard_normal((rows, hidden)).astype(np.float32)
+    w = _bf16(rng.standard_normal((vocab, hidden)) * 0.1)
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"], p["top_k"], p["top_p"], p["temperature"] = 1, 50, np.float32(0.95), np.float32(0.9)
+    p["rep_penalty"], p["supp_begin"], p["supp_end"], p["keep_id"], p["ban_id"] = np.float32(1.0), 2048, 3072, 2150, -1
+    u = rng.random(rows)
+    q, scale = _pack_on_gpu(ctx, w)
+    d_x, d_q, d_s = DeviceArray.from_numpy(x), DeviceArray.from_numpy(q), DeviceArray.from_numpy(scale)
+    d_logits = DeviceArray((rows, vocab), np.float32)
+    d_p, d_u, d_ids = DeviceArray.from_numpy(p), DeviceArray.from_numpy(u), DeviceArray((rows,), np.int32)
+    ctx.head_int8_device(rows, hidden, vocab, d_x, hidden, d_q, hidden, d_s, d_logits, vocab)
+    ctx.sample_device(rows, vocab, d_logits, vocab, d_p, 1, d_u, d_ids)
+    ctx.synchronize()
+    logits = d_logits.numpy()
+    assert np.all(np.abs(logits - head_int8_exact(x, q, scale)) <= head_int8_bound(x, q, scale))
+    ids = d_ids.numpy()
+    c = ref.classify(ids, ref.sample(logits, p, u))
+    assert c["unexplained"] == 0, c
