@@ -261,8 +261,9 @@ VXS_API int vxs_head_int8_device(vxs_ctx* ctx, int rows, int k, int n, const flo
  * int8 packing of a bf16 head weight on the GPU, PackedMatrix.FromBf16LinearInt8
  * (src/Voxwerk/Numerics/PackedMatrix.cs:124-154), bit for bit: per output row j, amax = max_k |W[j][k]|,
  * scale[j] = amax / 127 (1 when amax is 0), q[j][k] = clamp(round-half-even(W[j][k] * (1 / scale[j])),
- * -127, 127), in correctly rounded fp32. W bf16 [n][ldw], q int8 [n][ldq], scale fp32 [n]; finite
- * weights. Asynchronous on the context stream.
+ * -127, 127), in correctly rounded fp32, the (int) conversion saturating as in .NET 9 and later (a
+ * row whose 1 / scale overflows gets +-127 and 0). W bf16 [n][ldw], q int8 [n][ldq], scale fp32 [n];
+ * finite weights. Asynchronous on the context stream.
  */
 VXS_API int vxs_head_pack_int8_device(vxs_ctx* ctx, int k, int n, const uint16_t* d_w, int64_t ldw, int8_t* d_q,
                                       int64_t ldq, float* d_scale);

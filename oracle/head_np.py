@@ -43,10 +43,14 @@ def pack_int8(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """bf16 bits [N][K] -> (q int8 [N][K], scale fp32 [N]) as FromBf16LinearInt8 (PackedMatrix.cs:129-152)."""
     wf = widen(w)
     amax = np.max(np.abs(wf), axis=1)
-    scale = np.where(amax > 0, amax / np.float32(127.0), np.float32(1.0)).astype(np.float32)  # :142
-    inv = (np.float32(1.0) / scale).astype(np.float32)  # :143
-    prod = (wf * inv[:, None]).astype(np.float32)
-    q = np.clip(np.rint(prod), -127, 127).astype(np.int8)  # MathF.Round: ties to even (:146)
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+        scale = np.where(amax > 0, amax / np.float32(127.0), np.float32(1.0)).astype(np.float32)  # :142
+        inv = (np.float32(1.0) / scale).astype(np.float32)  # :143; inf when amax < ~3.7e-37
+        prod = (wf * inv[:, None]).astype(np.float32)
+        r = np.rint(prod)  # MathF.Round: ties to even (:146)
+    # (int) of a float saturates in .NET 9 and later: NaN -> 0, +-inf -> int.MaxValue / MinValue;
+    # then Math.Clamp to [-127, 127]
+    q = np.where(np.isnan(r), 0.0, np.clip(r, -127, 127)).astype(np.int8)
     return q, scale
 
 

@@ -151,6 +151,8 @@ def test_pack_int8_bit_exact(ctx, n, k, ldw, ldq):
         wf[1, :8] = [127.0, -63.5, 2.5, 3.5, -0.5, 0.0, 1.5, -126.5]  # ties at scale 1
         wf[1, 8:] = np.clip(wf[1, 8:], -100, 100)
         wf[2] = np.round(wf[2] * 4) / 4
+        wf[3] = 0.0  # a row whose inverse scale overflows (amax 2^-125): q saturates to +-127 / 0
+        wf[3, :4] = [2.0**-125, -(2.0**-125), 0.0, 2.0**-126]
     w = _bf16(wf)
     q, scale = _pack_on_gpu(ctx, w, ldw, ldq)
     wq, ws = pack_int8(w)

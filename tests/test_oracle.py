@@ -484,6 +484,18 @@ def test_pack_int8_hand_derived_rows():
     assert scale[3] == np.float32(0.25) / np.float32(127.0) and q[3].tolist()[:2] == [-127, 64]
 
 
+def test_pack_int8_row_whose_inverse_scale_overflows():
+    """amax below ~3.7e-37: scale = amax / 127 is tiny, 1 / scale overflows to +inf, so w * inf is
+    +-inf (or NaN for w = 0); .NET 9+ saturating (int) casts and the clamp give +-127 and 0."""
+    from oracle.head_np import pack_int8
+
+    tiny = np.float32(2.0**-125)  # normal; tiny / 127 is subnormal and 1 / that overflows
+    w = _bf16(np.array([[tiny, -tiny, 0.0, tiny / 2]], np.float32))
+    q, scale = pack_int8(w)
+    assert scale[0] == np.float32(tiny) / np.float32(127.0) and np.isinf(np.float32(1.0) / scale[0])
+    assert q[0].tolist() == [127, -127, 0, 127]
+
+
 def test_pack_int8_against_python_floats():
     """Per element in Python: the fp32 quotient and product as the correctly rounded value of the
     exact rational (fractions), round-half-even by Python's round(); differently computed."""

@@ -265,7 +265,9 @@ __global__ __launch_bounds__(kHT) void head_pack_i8_kernel(int k, const uint16_t
     int8_t* qr = q + (int64_t)n * ldq;
     for (int i = threadIdx.x; i < k; i += kHT) {
         const float t = rintf(__uint_as_float((uint32_t)row[i] << 16) * inv);  // half to even, as MathF.Round
-        qr[i] = (int8_t)min(max((int)t, -127), 127);
+        // (int) then Math.Clamp, with .NET's saturating conversion: NaN (0 * inf, when 1 / scale
+        // overflowed) gives 0, +-inf the clamp's ends; clamped in fp32 first, so the cast is exact
+        qr[i] = (int8_t)(t != t ? 0 : (int)fminf(fmaxf(t, -127.0f), 127.0f));
     }
     if (threadIdx.x == 0) scale[n] = scl;
 }
