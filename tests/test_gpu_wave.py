@@ -151,3 +151,25 @@ def test_wave_all_rows_handed_back(ctx):
     p["do_sample"], p["top_k"], p["top_p"], p["temperature"] = 1, 50, np.float32(0.95), np.float32(0.9)
     p["rep_penalty"], p["keep_id"], p["ban_id"] = np.float32(1.0), -1, -1
     run_both_paths(ctx, logits, p, rng.random(rows), label="all handed back")
+
+
+@pytest.mark.parametrize("seed", [11, 12, 13])
+def test_wave_full_batches_mixed(ctx, seed):
+    """4096-row batches (both halves of the launch, the second starting its loads later) with the
+    headline's full-vocabulary options varied per row: ids against the oracle and the block path."""
+    rng = np.random.default_rng(seed)
+    rows, vocab = 4096, 3072
+    mix = rng.random((rows, vocab)) < rng.uniform(0.02, 0.2, size=(rows, 1))
+    logits = (rng.standard_normal((rows, vocab)) * rng.choice([0.5, 1.0, 2.0], size=(rows, 1)) + 4.0 * mix)
+    logits = logits.astype(np.float32)
+    hl = rng.integers(0, 513, size=rows)
+    off = np.zeros(rows + 1, np.int32)
+    off[1:] = np.cumsum(hl)
+    hist = rng.integers(0, vocab, size=off[-1]).astype(np.int32)
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = 1
+    p["top_p"] = rng.choice([1.0, 0.98, 0.95, 0.9, 0.7], size=rows).astype(np.float32)
+    p["temperature"] = rng.choice([0.8, 1.0, 1.2], size=rows).astype(np.float32)
+    p["rep_penalty"] = rng.choice([1.0, 1.1, 1.3], size=rows).astype(np.float32)
+    p["keep_id"], p["ban_id"] = -1, -1
+    run_both_paths(ctx, logits, p, rng.random(rows), off, hist, label=f"4096 rows seed {seed}")
