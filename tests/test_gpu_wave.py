@@ -142,15 +142,15 @@ def test_wave_equal_mass_cuts(ctx):
     run_both_paths(ctx, x, p, u, label="equal-mass cuts")
 
 
-def test_wave_all_rows_handed_back(ctx):
-    """Every row samples with top-k, so the one-wave path flags every row for the general kernel."""
+def test_wave_all_rows_top_k(ctx):
+    """Every row samples with top-k 50 (the talker default), which the one-wave path now takes itself."""
     rng = np.random.default_rng(77)
     rows, vocab = 2050, 3072
     logits = (rng.standard_normal((rows, vocab)) * 2.5).astype(np.float32)
     p = np.zeros(rows, dtype=PARAMS_DTYPE)
     p["do_sample"], p["top_k"], p["top_p"], p["temperature"] = 1, 50, np.float32(0.95), np.float32(0.9)
     p["rep_penalty"], p["keep_id"], p["ban_id"] = np.float32(1.0), -1, -1
-    run_both_paths(ctx, logits, p, rng.random(rows), label="all handed back")
+    run_both_paths(ctx, logits, p, rng.random(rows), label="all top-k")
 
 
 @pytest.mark.parametrize("seed", [11, 12, 13])
@@ -173,3 +173,32 @@ def test_wave_full_batches_mixed(ctx, seed):
     p["rep_penalty"] = rng.choice([1.0, 1.1, 1.3], size=rows).astype(np.float32)
     p["keep_id"], p["ban_id"] = -1, -1
     run_both_paths(ctx, logits, p, rng.random(rows), off, hist, label=f"4096 rows seed {seed}")
+
+
+@pytest.mark.parametrize("vocab", [300, 1000, 2048, 3072])
+def test_wave_top_k_edges(ctx, vocab):
+    """Top-k on one wave at its edges: K = 1, 64 and 65 (the last handed back), logits quantised so
+    that ties at the k-th value push the candidates past 64 (handed back) or not, rows whose
+    suppression leaves fewer finite entries than K (no masking, the exact regime over them), and
+    top-p, temperature and penalty mixes; ids against the oracle and the block path."""
+    rng = np.random.default_rng(4000 + vocab)
+    rows = 1024
+    logits = (rng.standard_normal((rows, vocab)) * rng.choice([0.5, 2.0, 4.0], size=(rows, 1))).astype(np.float32)
+    quant = rng.random(rows) < 0.3
+    logits[quant] = np.round(logits[quant] * 2.0) / 2.0  # many exact ties
+    hl = rng.integers(0, 400, size=rows)
+    off = np.zeros(rows + 1, np.int32)
+    off[1:] = np.cumsum(hl)
+    hist = rng.integers(0, vocab, size=off[-1]).astype(np.int32)
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = 1
+    p["top_k"] = rng.choice([1, 2, 17, 50, 64, 65], size=rows)
+    p["top_p"] = rng.choice([1.0, 0.95, 0.8, 0.3], size=rows).astype(np.float32)
+    p["temperature"] = rng.choice([0.7, 0.9, 1.0], size=rows).astype(np.float32)
+    p["rep_penalty"] = rng.choice([1.0, 1.05, 1.3], size=rows).astype(np.float32)
+    few = rng.random(rows) < 0.15  # suppress all but a few dozen entries
+    p["supp_begin"] = np.where(few, 40, 0)
+    p["supp_end"] = np.where(few, vocab, 0)
+    p["keep_id"] = np.where(few, vocab - 1, -1)
+    p["ban_id"] = -1
+    run_both_paths(ctx, logits, p, rng.random(rows), off, hist, label=f"top-k edges V={vocab}")

@@ -6,8 +6,9 @@
 // histogram and a short ranking list, small enough for 16 rows per CU. The path covers what
 // full-vocabulary sampling needs — penalty, suppression, greedy, temperature, the nucleus regime
 // with or without top-p — and hands a row back untouched (return value 1) when it needs the general
-// algorithm: an active top-k, a history longer than 512 ids, at most 256 candidates (the exact
-// regime), a top-p cut whose crossing bucket holds more than 64 entries, a cut inside a group of
+// algorithm: a top-k above 64 or one whose entries at or above the k-th largest exceed 64, a history
+// longer than 512 ids, 65 to 256 candidates (the exact regime beyond one wave), a top-p cut whose
+// crossing bucket holds more than 64 entries, a cut inside a group of
 // equal masses far from where equal masses imply equal logits, a draw that finds no crossing, or a
 // call that asks for the write-back logits or the probabilities. Every decision depends on the row
 // alone, so results do not depend on the batch.
@@ -130,7 +131,7 @@ __device__ __forceinline__ int wave_prepare(const SampleArgs& a, int r, int lane
     using namespace wave;
     // outputs, the penalty alone and resident stores (whose step ends in put_id) take the general path
     if (a.out_logits || a.out_probs || (a.kflags & KF_STOP_AFTER_PENALTY) || a.store) return 1;
-    if (P.do_sample && P.top_k > 0 && P.top_k < a.vocab) return 1;
+    if (P.do_sample && P.top_k > kL && P.top_k < a.vocab) return 1;  // top-k beyond one wave's candidates
     const bool pen_on = P.rep_penalty != 1.0f && has_history(a);
     HistRange hr{0, 0};
     if (pen_on) hr = history_range(a, r);
@@ -274,6 +275,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
     float mx, mn;  // max; min including -inf
     float fmn;     // min over finite entries
     uint32_t cnt;  // finite entries
+    float lmx;     // this lane's maximum
     {
         // the NaN-propagating maximum turns a NaN or +inf anywhere in a lane into a non-finite max
         float tmx = v[0], tmn = v[0];
@@ -287,6 +289,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
             if (lane == 0) a.out_ids[r] = VXS_ERR_NONFINITE;
             return 0;
         }
+        lmx = tmx;
         mx = wave_fmax(tmx);
         if (pen_on && (mx >= 0x1p100f || (mx > 0.0f && mx < 0x1p-30f))) return 1;  // see S1
         mn = wave_fmin(tmn);
@@ -309,7 +312,117 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         if (lane == 0) a.out_ids[r] = V - 1;
         return 0;
     }
-    if (cnt <= (uint32_t)kExact) return 1;  // exact regime
+    // ================= top-k and the exact regime on one wave =================
+    // Rows whose candidates fit one wave: top-k with K <= 64 (the entries >= the k-th largest, ties
+    // kept), or at most 64 finite entries. The entries above a lower bound of the k-th largest (the
+    // k-th largest lane maximum: at least K entries reach it) are gathered in index order (at most
+    // kCand), the exact k-th largest among them is found by bisection over their keys, and the
+    // reference's fp64 arithmetic runs on the final candidates, one per lane (wave_exact).
+    const int K = P.top_k;
+    const bool topk_on = K > 0 && K < V && (uint32_t)K < cnt;  // else top-k masks nothing (Sampler.cs:42)
+    if (topk_on || cnt <= (uint32_t)kL) {
+        constexpr int kCand = 256;
+        float* cval = sm.u.xs;                                             // gathered values
+        int32_t* cidx = reinterpret_cast<int32_t*>(sm.u.xs + kCand);       // ... and their indices
+        float* fx = sm.u.xs + 2 * kCand;                                   // final candidates
+        int32_t* fid = reinterpret_cast<int32_t*>(sm.u.xs + 2 * kCand + kL);
+        double* scr = reinterpret_cast<double*>(sm.u.xs + 2 * kCand + 2 * kL);  // wave_exact's 192 doubles
+        // lower bound: the K-th largest lane maximum (exact unless ties), or every finite entry
+        float tf = -3.402823466e38f;
+        if (topk_on) {
+            const uint32_t lk[1] = {f2key(lmx)};
+            tf = key2f(wave_bound_regs<1>(lk, wave_umin(lk[0]), wave_umax(lk[0]), K, 0));
+        }
+        // gather the entries >= tf in index order: per sweep, each lane's count (0..4) in a 16-bit
+        // field, four sweeps per 64-bit scan
+        constexpr int NH = (NS + 3) / 4;
+        uint64_t exc[NH], tot[NH];
+#pragma unroll
+        for (int h = 0; h < NH; h++) {
+            uint64_t mine = 0;
+#pragma unroll
+            for (int c = 4 * h; c < NS && c < 4 * h + 4; c++) {
+                uint32_t m = 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) m += v[c * 4 + j] >= tf ? 1u : 0u;
+                mine |= (uint64_t)m << (16 * (c - 4 * h));
+            }
+            const uint64_t incl = wave_incl_sum(mine);
+            exc[h] = incl - mine;
+            tot[h] = readlane64(incl, 63);
+        }
+        uint32_t n = 0;
+#pragma unroll
+        for (int c = 0; c < NS; c++) {
+            const int f = 16 * (c % 4);
+            uint32_t off = n + (uint32_t)((exc[c / 4] >> f) & 0xffffu);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int e = c * 4 + j;
+                if (v[e] >= tf) {
+                    if (off < (uint32_t)kCand) {
+                        cval[off] = v[e];
+                        cidx[off] = eidx(e);
+                    }
+                    off++;
+                }
+            }
+            n += (uint32_t)((tot[c / 4] >> f) & 0xffffu);
+        }
+        if (n > (uint32_t)kCand) return 1;  // too many entries above the bound: general path
+        wsync();
+        uint32_t nf = n;
+        if (topk_on) {
+            // the exact k-th largest key among the gathered entries (all entries >= it are here)
+            uint32_t kq[4];
+            float cv[4];
+            int32_t ci[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int pq = lane + 64 * q;
+                const bool in = pq < (int)n;
+                cv[q] = in ? cval[pq] : 0.0f;
+                ci[q] = in ? cidx[pq] : 0;
+                kq[q] = in ? f2key(cv[q]) : 0u;
+            }
+            uint32_t lo = f2key(tf), hi = f2key(mx);
+#pragma unroll 1
+            while (lo < hi) {
+                const uint32_t mid = lo + ((hi - lo + 1) >> 1);
+                int c = 0;
+#pragma unroll
+                for (int q = 0; q < 4; q++) c += __builtin_popcountll(__ballot(kq[q] >= mid));
+                if (c >= K) lo = mid;
+                else hi = mid - 1;
+            }
+            // the final candidates (>= the k-th largest), still in index order
+            nf = 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const bool keep = kq[q] >= lo;  // empty slots hold 0 < lo
+                const uint64_t bal = __ballot(keep);
+                if (keep) {
+                    const uint32_t pos = nf + mbcnt(bal);
+                    if (pos < (uint32_t)kL) {
+                        fx[pos] = cv[q];
+                        fid[pos] = ci[q];
+                    }
+                }
+                nf += (uint32_t)__builtin_popcountll(bal);
+            }
+            if (nf > (uint32_t)kL) return 1;  // ties at the k-th value beyond one wave
+            wsync();
+        } else {
+            fx = cval;  // at most 64 finite entries: every one is a candidate
+            fid = cidx;
+        }
+        const double uu = a.u ? a.u[r] : 0.0;
+        const float xl = lane < (int)nf ? fx[lane] : 0.0f;
+        const int pick = wave_exact(xl, fid, (int)nf, mx, P.top_p < 1.0f, P.top_p, uu, scr, nullptr, lane);
+        if (lane == 0) a.out_ids[r] = pick;
+        return 0;
+    }
+    if (cnt <= (uint32_t)kExact) return 1;  // exact regime beyond one wave
 
     // ================= nucleus regime =================
     const double u = a.u ? a.u[r] : 0.0;
