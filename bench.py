@@ -373,6 +373,54 @@ def measure_device(ctx, w, steps: int, warmup: int, hip, np) -> dict:
             "_batch": b}
 
 
+def measure_talker_topk(ctx, top_p: float, steps: int, hip, np, check: bool) -> dict:
+    """A talker stage at serving scale on the device path: 4096 rows x 3072, top-k 50, temperature
+    0.9, penalty 1.05 over 256-id histories, suppression of [2048, 3072) except 2150, the given
+    top-p (the talker's options, TalkerGenerator.cs:244-249, over a batch); logits N(0, 3^2), seed 5.
+    Inputs rotated over 12 copies (beyond the last-level cache); HIP events on the context stream;
+    with `check`, every row's id classified against the CPU oracle."""
+    from voxwerk_amd._lib import PARAMS_DTYPE
+
+    rng = np.random.default_rng(5)
+    rows, V, H = 4096, 3072, 256
+    x = (rng.standard_normal((rows, V)) * 3.0).astype(np.float32)
+    off = (np.arange(rows + 1) * H).astype(np.int32)
+    hist = rng.integers(0, 2048, size=rows * H).astype(np.int32)
+    p = np.zeros(1, dtype=PARAMS_DTYPE)
+    p["do_sample"], p["top_k"], p["top_p"], p["temperature"] = 1, 50, np.float32(top_p), np.float32(0.9)
+    p["rep_penalty"], p["supp_begin"], p["supp_end"], p["keep_id"], p["ban_id"] = np.float32(1.05), 2048, 3072, 2150, -1
+    u = rng.random(rows)
+    nbuf = 12
+    d_x = [hip.DeviceArray.from_numpy(x) for _ in range(nbuf)]
+    d_h, d_o = hip.DeviceArray.from_numpy(hist), hip.DeviceArray.from_numpy(off)
+    d_p, d_u, d_ids = hip.DeviceArray.from_numpy(p), hip.DeviceArray.from_numpy(u), hip.DeviceArray((rows,), np.int32)
+    for i in range(max(10, steps // 10)):
+        ctx.sample_device(rows, V, d_x[i % nbuf], V, d_p, 0, d_u, d_ids, d_o, d_h)
+    hip.synchronize()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(ctx.stream())
+    for i in range(steps):
+        ctx.sample_device(rows, V, d_x[i % nbuf], V, d_p, 0, d_u, d_ids, d_o, d_h)
+    e1.record(ctx.stream())
+    e1.synchronize()
+    us = e0.elapsed_ms(e1) / steps * 1e3
+    ids = d_ids.numpy()
+    for a in d_x:
+        a.free()
+    nbytes = rows * (4 * V + 4 * H + 4 + 8 + 4)
+    gbps = nbytes / (us * 1e-6) / 1e9
+    m = {"workload": f"talker_topk {rows}x{V}, top-k 50, top-p {top_p}, T 0.9, penalty 1.05 over {H} ids, "
+                     f"suppression [2048, 3072) but 2150, device-resident ({nbuf} rotating copies)",
+         "us_per_step": round(us, 3), "rows_per_s": round(rows / (us * 1e-6), 1), "algorithmic_bytes": nbytes,
+         "hbm_gbps": round(gbps, 1), "hbm_pct_peak": round(100 * gbps / HBM_PEAK_GBPS, 2)}
+    if check:
+        from oracle import ref
+
+        o = ref.sample(x, np.broadcast_to(p, (rows,)).copy(), u, off, hist, threads=os.cpu_count() or 1)
+        m["parity"] = ref.classify(ids, o)
+    return m
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -546,6 +594,12 @@ def main() -> int:
             extra[workloads.NAMES[wid]] = m
             log(f"[bench] {m['workload']}: {m['us_per_step']:.2f} us/step, {m['rows_per_s']:.4g} rows/s, "
                 f"{m['hbm_gbps']:.0f} GB/s")
+        # the talker stage at serving scale (top-k on the one-wave path)
+        for tp in (1.0, 0.95):
+            m = measure_talker_topk(ctx, tp, 1000, hip, np, not args.no_cpu)
+            extra[f"talker_topk_p{tp}"] = m
+            log(f"[bench] {m['workload']}: {m['us_per_step']:.2f} us/step, {m['rows_per_s']:.4g} rows/s"
+                + (f", parity {m['parity']}" if "parity" in m else ""))
         # code-predictor frame: 15 dependent 16x2048 steps, host to host
         w2 = workloads.workload(2)
         steps2 = [w2.generate(step=k) for k in range(w2.steps)]

@@ -218,8 +218,8 @@ int choose_path(uint32_t flags, int rows, int vocab) {
     return rows >= 1024 ? vxs::kPathQuad : vxs::kPathBlock;
 }
 
-// Host calls know their options: when most rows sample with top-k, which the one-wave path always
-// hands back, go to the one-workgroup-per-row kernel directly.
+// Host calls know their options: when most rows sample with a top-k above 64, which the one-wave
+// path hands back, go to the one-workgroup-per-row kernel directly.
 int choose_path_host(uint32_t flags, int rows, int vocab, const vxs_params* params, int stride) {
     const int path = choose_path(flags, rows, vocab);
     if (path != vxs::kPathQuad || (flags & VXS_FLAG_PATH_WAVE)) return path;
@@ -227,7 +227,7 @@ int choose_path_host(uint32_t flags, int rows, int vocab, const vxs_params* para
     int topk = 0;
     for (int i = 0; i < np; i++) {
         const vxs_params& p = params[(int64_t)i * stride];
-        topk += p.do_sample && p.top_k > 0 && p.top_k < vocab;
+        topk += p.do_sample && p.top_k > vxs::kWaveMaxTopK && p.top_k < vocab;
     }
     return 2 * topk > np ? vxs::kPathBlock : path;
 }

@@ -74,6 +74,8 @@ enum : int {
 constexpr int kRowResidentMaxVocab = 8192;
 // Largest vocabulary of the one-wave-per-row fast path (vxs_wave.h).
 constexpr int kWaveMaxVocab = 3072;
+// Largest top-k the one-wave path samples itself (its final candidates are one per lane).
+constexpr int kWaveMaxTopK = 64;
 // Largest vocabulary of the streaming kernel (vxs_wide.hip); its history bitmap lives in LDS.
 constexpr int kWideMaxVocab = 1 << 19;
 

@@ -45,7 +45,8 @@ constexpr int kPart = 6;     // sweeps staged in LDS at once for the penalty
 constexpr int kNB = 1024;    // top-p histogram buckets (16 per lane)
 constexpr int kBPL = kNB / 64;
 static_assert(kNB == 1024, "bucket index is a 10-bit field of the mass bits");
-constexpr int kL = 64;       // crossing-bucket entries ranked exactly (one per lane)
+constexpr int kL = 64;       // crossing-bucket entries ranked exactly (one per lane); top-k bound
+static_assert(kL == kWaveMaxTopK, "the one-wave top-k capacity is its lane count");
 constexpr int kExact = 256;  // rows with at most this many candidates take the exact regime
 constexpr int kHP = 8;       // history ids per lane fetched with the row (512 per row)
 
