@@ -616,7 +616,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 // they add nothing to any sum, sort first in the top-p order (where the loop passes over them) and
 // are never drawn. The sequential sums read their terms from LDS in batches (the reads of a batch
 // issued before its adds), every lane adding the same terms in the reference's order; ranks and the
-// crossings are found in register batches. scr: 192 doubles of wave-private LDS. Returns the sampled id
+// crossings are found in register batches. scr: 193 doubles of wave-private LDS. Returns the sampled id
 // (uniform); with prow, lanes < n store their final probability to prow[ids[lane]].
 __device__ __forceinline__ int wave_exact(float x, const int32_t* ids, int n, float m, bool topp, float top_p,
                                           double u, double* scr, double* prow, int lane) {
@@ -652,6 +652,7 @@ __device__ __forceinline__ int wave_exact(float x, const int32_t* ids, int n, fl
             const u64x2 q = kp[l / 2];
             rank += (q.x < k ? 1 : 0) + (q.y < k ? 1 : 0);
         }
+    }
     }
     wave_lds_sync();  // every lane has read the keys
     int* at = reinterpret_cast<int*>(key);

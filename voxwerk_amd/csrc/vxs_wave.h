@@ -327,7 +327,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         int32_t* cidx = reinterpret_cast<int32_t*>(sm.u.xs + kCand);       // ... and their indices
         float* fx = sm.u.xs + 2 * kCand;                                   // final candidates
         int32_t* fid = reinterpret_cast<int32_t*>(sm.u.xs + 2 * kCand + kL);
-        double* scr = reinterpret_cast<double*>(sm.u.xs + 2 * kCand + 2 * kL);  // wave_exact's 192 doubles
+        double* scr = reinterpret_cast<double*>(sm.u.xs + 2 * kCand + 2 * kL);  // wave_exact's 193 doubles
         // lower bound: the K-th largest lane maximum (exact unless ties), or every finite entry
         float tf = -3.402823466e38f;
         if (topk_on) {
