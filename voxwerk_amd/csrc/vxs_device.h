@@ -653,7 +653,6 @@ __device__ __forceinline__ int wave_exact(float x, const int32_t* ids, int n, fl
             rank += (q.x < k ? 1 : 0) + (q.y < k ? 1 : 0);
         }
     }
-    }
     wave_lds_sync();  // every lane has read the keys
     int* at = reinterpret_cast<int*>(key);
     if (in) {
