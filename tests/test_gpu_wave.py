@@ -202,3 +202,34 @@ def test_wave_top_k_edges(ctx, vocab):
     p["keep_id"] = np.where(few, vocab - 1, -1)
     p["ban_id"] = -1
     run_both_paths(ctx, logits, p, rng.random(rows), off, hist, label=f"top-k edges V={vocab}")
+
+
+def test_wave_long_histories(ctx):
+    """Histories of 513 to 2048 ids on the one-wave path (taken in chunks, kept distinct by an LDS
+    bitmap), with ids repeated within and across chunks, rows whose bad id sits past the first 512,
+    and histories over 2048 (handed back): ids against the oracle and the block path."""
+    rng = np.random.default_rng(808)
+    rows, vocab = 1024, 3072
+    logits = (rng.standard_normal((rows, vocab)) * 2.5).astype(np.float32)
+    hl = rng.integers(400, 2300, size=rows)
+    off = np.zeros(rows + 1, np.int32)
+    off[1:] = np.cumsum(hl)
+    hist = np.empty(off[-1], np.int32)
+    for r in range(rows):
+        pool = rng.integers(0, vocab, size=rng.choice([40, 600, 3000]))  # few distinct ids: many repeats
+        hist[off[r]:off[r + 1]] = rng.choice(pool, size=hl[r])
+    bad_rows = rng.choice(rows, 12, replace=False)
+    for r in bad_rows:
+        if hl[r] > 600:
+            hist[off[r] + 550 + (r % 40)] = vocab + (r % 3)  # outside the vocabulary, past the first chunk
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = 1
+    p["top_k"] = rng.choice([0, 0, 50], size=rows)
+    p["top_p"] = rng.choice([1.0, 0.95, 0.8], size=rows).astype(np.float32)
+    p["temperature"] = rng.choice([0.9, 1.0], size=rows).astype(np.float32)
+    p["rep_penalty"] = rng.choice([1.05, 1.3, 0.8], size=rows).astype(np.float32)
+    p["keep_id"], p["ban_id"] = -1, -1
+    wave, _ = run_both_paths(ctx, logits, p, rng.random(rows), off, hist, label="long histories")
+    for r in bad_rows:
+        if hl[r] > 600:
+            assert wave[r] == -2, (r, wave[r])  # VXS_ERR_ID_OUT_OF_RANGE

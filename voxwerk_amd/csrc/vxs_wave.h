@@ -7,7 +7,7 @@
 // full-vocabulary sampling needs — penalty, suppression, greedy, temperature, the nucleus regime
 // with or without top-p — and hands a row back untouched (return value 1) when it needs the general
 // algorithm: a top-k above 64 or one whose entries at or above the k-th largest exceed 64, a history
-// longer than 512 ids, 65 to 256 candidates (the exact regime beyond one wave), a top-p cut whose
+// longer than 2048 ids, 65 to 256 candidates (the exact regime beyond one wave), a top-p cut whose
 // crossing bucket holds more than 64 entries, a cut inside a group of
 // equal masses far from where equal masses imply equal logits, a draw that finds no crossing, or a
 // call that asks for the write-back logits or the probabilities. Every decision depends on the row
@@ -49,6 +49,7 @@ constexpr int kL = 64;       // crossing-bucket entries ranked exactly (one per 
 static_assert(kL == kWaveMaxTopK, "the one-wave top-k capacity is its lane count");
 constexpr int kExact = 256;  // rows with at most this many candidates take the exact regime
 constexpr int kHP = 8;       // history ids per lane fetched with the row (512 per row)
+constexpr int kHMax = 2048;  // longest history the wave path takes (the rest in chunks of 8 per lane)
 
 typedef double dbl2 __attribute__((ext_vector_type(2)));
 
@@ -86,7 +87,8 @@ __device__ __forceinline__ uint32_t mbcnt(uint64_t bal) {
 template <int NS>
 struct WaveSmem {
     union {
-        float xs[wave::kPart * wave::kSweep + 64];  // penalty staging, then one spare slot per lane
+        // penalty staging, one spare slot per lane, then a 4096-bit id bitmap for long histories
+        float xs[wave::kPart * wave::kSweep + 64 + 128];
         wave::Sel sel;
     } u;
 };
@@ -139,7 +141,7 @@ __device__ __forceinline__ int wave_prepare(const SampleArgs& a, int r, int lane
     w.pen_on = pen_on;  // each field written once: no selected-address stores
     w.h0 = hr.h0;
     w.h1 = hr.h1;
-    if (hr.h1 - hr.h0 > kHP * 64) return 1;  // long history
+    if (hr.h1 - hr.h0 > kHMax) return 1;  // very long history
     if (pen_on) {
 #pragma unroll
         for (int k = 0; k < kHP; k++) {
@@ -185,6 +187,65 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         const float arho = __builtin_fabsf(rho);
         if (!(arho >= 0x1p-20f && arho <= 0x1p20f)) return 1;
         const float rinv = 1.0f / rho;
+        float* xs = sm.u.xs;
+        typedef float f4 __attribute__((ext_vector_type(4)));
+        if (h1 - h0 > kHP * 64) {
+            // A history over 512 ids: the ids are taken in chunks of eight per lane (the first chunk
+            // fetched with the row), and an LDS bitmap keeps them distinct: the lane whose atomicOr
+            // first sets an id's bit penalises that entry of the staged part. Per part, every id is
+            // tested; an id outside the vocabulary fails the row (checked over all ids in part 0).
+            uint32_t* bm = reinterpret_cast<uint32_t*>(xs + kPart * kSweep + 64);
+            typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+            *(u2v*)&bm[2 * lane] = u2v{0u, 0u};  // 128 words: 4096 bits
+#pragma unroll
+            for (int p0 = 0; p0 < NS; p0 += kPart) {
+#pragma unroll
+                for (int c = 0; c < kPart; c++)
+                    if (p0 + c < NS)
+                        *(f4*)(xs + c * kSweep + lane4) =
+                            f4{v[(p0 + c) * 4 + 0], v[(p0 + c) * 4 + 1], v[(p0 + c) * 4 + 2], v[(p0 + c) * 4 + 3]};
+                wsync();
+                const int lo = p0 * kSweep, span = (p0 + kPart < NS ? kPart : NS - p0) * kSweep;
+                bool bad = false;
+#pragma unroll 1
+                for (int k0 = 0; k0 < kHMax / 64; k0 += kHP) {
+                    if (h0 + 64 * k0 >= h1) break;  // uniform: no ids left
+                    int id[kHP];
+#pragma unroll
+                    for (int k = 0; k < kHP; k++) {
+                        const int h = h0 + lane + 64 * (k0 + k);
+                        id[k] = k0 == 0 ? pre[k] : (h < h1 ? a.hist_ids[h] : 0);
+                    }
+#pragma unroll
+                    for (int k = 0; k < kHP; k++) {
+                        const bool lv = h0 + lane + 64 * (k0 + k) < h1;
+                        bad |= lv && (unsigned)id[k] >= (unsigned)V;
+                        if (lv && (unsigned)id[k] < (unsigned)V && (unsigned)(id[k] - lo) < (unsigned)span) {
+                            const uint32_t bit = 1u << (id[k] & 31);
+                            if (!(atomicOr(&bm[id[k] >> 5], bit) & bit)) {
+                                float* px = xs + (id[k] - lo);
+                                *px = penalize_fast(*px, rho, rinv);
+                            }
+                        }
+                    }
+                }
+                if (p0 == 0 && __ballot(bad)) {
+                    if (lane == 0) a.out_ids[r] = VXS_ERR_ID_OUT_OF_RANGE;
+                    return 0;
+                }
+                wsync();
+#pragma unroll
+                for (int c = 0; c < kPart; c++)
+                    if (p0 + c < NS) {
+                        const f4 q = *(const f4*)(xs + c * kSweep + lane4);
+                        v[(p0 + c) * 4 + 0] = q.x;
+                        v[(p0 + c) * 4 + 1] = q.y;
+                        v[(p0 + c) * 4 + 2] = q.z;
+                        v[(p0 + c) * 4 + 3] = q.w;
+                    }
+                wsync();  // the next part (or phase) overwrites the staging area
+            }
+        } else {
         bool live[kHP];
         bool bad = false;
 #pragma unroll
@@ -196,8 +257,6 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
             if (lane == 0) a.out_ids[r] = VXS_ERR_ID_OUT_OF_RANGE;
             return 0;
         }
-        float* xs = sm.u.xs;
-        typedef float f4 __attribute__((ext_vector_type(4)));
 #pragma unroll
         for (int p0 = 0; p0 < NS; p0 += kPart) {
 #pragma unroll
@@ -230,6 +289,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
                     v[(p0 + c) * 4 + 3] = q.w;
                 }
             wsync();  // the next part (or phase) overwrites the staging area
+        }
         }
     }
 
