@@ -147,8 +147,8 @@ VXS_API int vxs_sample_noalloc(vxs_ctx* ctx, int rows, int vocab, const float* l
 
 /*
  * Parity/debug variant of vxs_sample_device (no counterpart in the reference): no write-back or
- * probabilities; instead, for every row sampled by the one-wave nucleus regime (the wave path's
- * own work: sampled rows without top-k, vocab <= 3072),
+ * probabilities; instead, for every row sampled by the one-wave nucleus regime (sampled rows,
+ * vocab <= 3072, whose top-k masks nothing and that keep more than 256 finite entries),
  *   d_stats[4r + 0] = kept fraction of the probability mass (after top-p; 1 without top-p),
  *   d_stats[4r + 1] = smallest kept probability (the top-p cut),
  *   d_stats[4r + 2] = number of kept entries (entries whose mass is 0 on the 2^-F grid excluded),
