@@ -266,19 +266,46 @@ def summarize_trace(path: str) -> None:
     import csv
     from collections import defaultdict
 
-    groups = defaultdict(list)
+    # Launches in time order; a (kernel, grid) that recurs after other launches starts a new
+    # segment (#2, #3, ...), so that workloads sharing a kernel and grid are reported apart.
+    launches = []
     with open(path, newline="") as f:
         for row in csv.DictReader(f):
             name = row.get("Kernel_Name") or row.get("KernelName") or row.get("Name")
             grid = row.get("Grid_Size_X") or row.get("Grid_Size") or "?"
             wg = row.get("Workgroup_Size_X") or row.get("Workgroup_Size") or "?"
-            dur = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
-            groups[(name, grid, wg)].append(dur)
+            t0, t1 = int(row["Start_Timestamp"]), int(row["End_Timestamp"])
+            launches.append((t0, t1 - t0, (name, grid, wg)))
+    launches.sort()
+    groups = defaultdict(list)  # (key, segment) -> durations; segments of fewer than 50 launches pooled
+    first = {}
+    seg = defaultdict(int)
+    last = None
+    runs = []
+    for t0, dur, key in launches:
+        if key != last:
+            seg[key] += 1
+            last = key
+        runs.append((t0, dur, key, seg[key]))
+    sizes = defaultdict(int)
+    for _, _, key, sg in runs:
+        sizes[(key, sg)] += 1
+    for t0, dur, key, sg in runs:
+        g = (key, sg if sizes[(key, sg)] >= 50 else 0)
+        groups[g].append(dur)
+        first.setdefault(g, t0)
+    # label the groups of a kernel run 1, 2, ... in time order when it has more than one
+    label = {}
+    for key in {k for k, _ in groups}:
+        gs = sorted((first[g], g) for g in groups if g[0] == key)
+        for i, (_, g) in enumerate(gs):
+            label[g] = f" [run {i + 1} of {len(gs)}]" if len(gs) > 1 else ""
     print(f"{'calls':>7} {'avg_us':>10} {'median_us':>10} {'min_us':>9} {'max_us':>9}  grid  wg  kernel")
-    for (name, grid, wg), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+    for g, d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        (name, grid, wg), _ = g
         d.sort()
         print(f"{len(d):7d} {sum(d) / len(d) / 1e3:10.3f} {d[len(d) // 2] / 1e3:10.3f} {d[0] / 1e3:9.3f} "
-              f"{d[-1] / 1e3:9.3f}  {grid}  {wg}  {name[:110]}")
+              f"{d[-1] / 1e3:9.3f}  {grid}  {wg}  {name[:110]}{label[g]}")
 
 
 def _read_pmc(path: str):
