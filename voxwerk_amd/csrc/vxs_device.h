@@ -603,6 +603,28 @@ __device__ __forceinline__ int wave_draw(const double* p, const int32_t* id, int
     return last >= 0 ? id[last] : 0;
 }
 
+// The draw over q (lane j: candidate j in index order, `keep` for p > 0) by a wave prefix sum in
+// place of the sequential running sum. q is p / s with s any fp64 sum of the kept p (or p itself
+// when it was already divided by the reference's sum); both the sequential loop's running sums and
+// the scan's lie within 64 * 2^-52 of the exact partial sums of p / (exact sum p), relative to 1
+// (at most 64 terms, each sum within gamma_63 of its exact value in any order, one rounding per
+// quotient), so a crossing that clears u by more than 2^-40 is the sequential loop's crossing, and
+// u clearing every kept sum by that much means no crossing (the last kept entry is drawn).
+// Returns the lane drawn, or -1 when u lies within 2^-40 of a deciding sum or a value is not finite:
+// the caller then runs the sequential form.
+__device__ __forceinline__ int wave_draw_par(double q, bool keep, double u) {
+    constexpr double kBand = 0x1p-40;
+    const double c = wave_incl_sum(keep ? q : 0.0);
+    const uint64_t kb = __ballot(keep);
+    const uint64_t bad = __ballot(keep && !(q <= 1.0));  // NaN or beyond 1
+    const uint64_t sure = __ballot(keep && u < c - kBand);
+    const uint64_t maybe = __ballot(keep && u < c + kBand);
+    if (bad || !kb) return -1;
+    if (!maybe) return !(u >= 0.0) ? -1 : 63 - __builtin_clzll(kb);
+    if (sure && __builtin_ctzll(sure) == __builtin_ctzll(maybe)) return __builtin_ctzll(sure);
+    return -1;
+}
+
 // LDS ordering inside one wave.
 __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -616,7 +638,10 @@ __device__ __forceinline__ void wave_lds_sync() {
 // they add nothing to any sum, sort first in the top-p order (where the loop passes over them) and
 // are never drawn. The sequential sums read their terms from LDS in batches (the reads of a batch
 // issued before its adds), every lane adding the same terms in the reference's order; ranks and the
-// crossings are found in register batches. scr: 193 doubles of wave-private LDS. Returns the sampled id
+// crossings are found in register batches. The first sum (the divisor of every probability) is
+// always the sequential one; the draw, and without prow the second sum before it, are decided by
+// wave sums (wave_draw_par) unless u lies within their rounding band of a deciding running sum,
+// when the sequential forms run. scr: 193 doubles of wave-private LDS. Returns the sampled id
 // (uniform); with prow, lanes < n store their final probability to prow[ids[lane]].
 __device__ __forceinline__ int wave_exact(float x, const int32_t* ids, int n, float m, bool topp, float top_p,
                                           double u, double* scr, double* prow, int lane) {
@@ -631,6 +656,8 @@ __device__ __forceinline__ int wave_exact(float x, const int32_t* ids, int n, fl
     p = in ? p / seq_sum_pipe(cp, n) : 0.0;  // :58-60, the sum in index order
     if (!topp) {
         if (prow && in) prow[ids[lane]] = p;
+        const int jp = wave_draw_par(p, in && !(p <= 0.0), u);
+        if (jp >= 0) return ids[jp];
         cp[lane] = p;
         wave_lds_sync();
         return wave_draw(cp, ids, n, u);  // :77-87
@@ -680,6 +707,11 @@ __device__ __forceinline__ int wave_exact(float x, const int32_t* ids, int n, fl
     // The entries left with p > 0 (or NaN), in index order: the second sum and the draw over them
     // alone are the reference's over all n (adding zero changes no sum; the draw skips p <= 0).
     const bool keep = in && !(p <= 0.0);
+    if (!prow) {  // the draw decided by a parallel sum and scan (the probabilities are not returned)
+        const double s2p = wave_sum(keep ? p : 0.0);
+        const int jp = wave_draw_par(keep ? p / s2p : 0.0, keep, u);
+        if (jp >= 0) return ids[jp];
+    }
     const uint64_t kb = __ballot(keep);
     const int nk = (int)__builtin_popcountll(kb);
     const int pos = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(kb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)kb, 0u));
