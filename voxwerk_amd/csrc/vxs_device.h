@@ -610,13 +610,14 @@ __device__ __forceinline__ int wave_draw(const double* p, const int32_t* id, int
 // (at most 64 terms, each sum within gamma_63 of its exact value in any order, one rounding per
 // quotient), so a crossing that clears u by more than 2^-40 is the sequential loop's crossing, and
 // u clearing every kept sum by that much means no crossing (the last kept entry is drawn).
-// Returns the lane drawn, or -1 when u lies within 2^-40 of a deciding sum or a value is not finite:
-// the caller then runs the sequential form.
+// Returns the lane drawn, or -1 when u lies within 2^-40 of a deciding sum, u is NaN or a kept q is
+// not in (0, 1]: the caller then runs the sequential form.
 __device__ __forceinline__ int wave_draw_par(double q, bool keep, double u) {
     constexpr double kBand = 0x1p-40;
     const double c = wave_incl_sum(keep ? q : 0.0);
     const uint64_t kb = __ballot(keep);
-    const uint64_t bad = __ballot(keep && !(q <= 1.0));  // NaN or beyond 1
+    // NaN, beyond 1, or a kept p whose quotient underflowed to 0 (the reference's draw skips it)
+    const uint64_t bad = __ballot(keep && !(q > 0.0 && q <= 1.0));
     const uint64_t sure = __ballot(keep && u < c - kBand);
     const uint64_t maybe = __ballot(keep && u < c + kBand);
     if (bad || !kb) return -1;
