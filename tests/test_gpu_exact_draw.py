@@ -70,3 +70,24 @@ def test_exact_draw_on_running_sums(ctx, vocab, top_p):
     ids_seq, _, probs2 = ctx.sample(x, p, u, want_probs=True, path="block")
     assert np.array_equal(ids_seq, want)
     assert np.array_equal(probs2, probs)
+
+
+@pytest.mark.parametrize("top_p", [1.0, 0.9])
+def test_exact_draw_out_of_range_uniforms(ctx, top_p):
+    """u outside [0, 1) (a caller's, never NextDouble's): the reference's loop still defines the id
+    (u >= every running sum or NaN: the last entry with p > 0; u < 0: the first), and the wave-sum
+    draw must give it on both paths."""
+    rows, vocab = 64, 2048
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((rows, vocab)) * 2.5).astype(np.float32)
+    p = np.zeros(1, dtype=PARAMS_DTYPE)
+    p["do_sample"], p["top_k"], p["top_p"], p["temperature"] = 1, 50, np.float32(top_p), np.float32(0.9)
+    p["rep_penalty"], p["keep_id"], p["ban_id"] = np.float32(1.0), -1, -1
+    _, _, probs = ctx.sample(x, p, rng.random(rows), want_probs=True, path="block")
+    u = np.array([(1.0, 1.5, np.nan, -0.5, np.inf, -np.inf)[r % 6] for r in range(rows)], dtype=np.float64)
+    want = np.array([sequential_draw(probs[r], u[r]) for r in range(rows)], dtype=np.int32)
+    kept = [np.flatnonzero(probs[r] > 0.0) for r in range(rows)]
+    assert all(want[r] == (kept[r][0] if u[r] < 0 else kept[r][-1]) for r in range(rows))
+    for path in ("block", "wave"):
+        got = ctx.sample(x, p, u, path=path)
+        assert np.array_equal(got, want), f"{path}: rows {np.flatnonzero(got != want)[:10].tolist()}"
