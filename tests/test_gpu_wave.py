@@ -175,6 +175,36 @@ def test_wave_full_batches_mixed(ctx, seed):
     run_both_paths(ctx, logits, p, rng.random(rows), off, hist, label=f"4096 rows seed {seed}")
 
 
+@pytest.mark.parametrize("seed,vocab", [(0, 1000), (1, 2048), (2, 2500), (3, 3072)])
+def test_wave_random_option_mix(ctx, seed, vocab):
+    """2048 rows whose options are drawn per row over everything the one-wave path takes or hands
+    back: greedy rows, top-k 1..80 on 60 % of the rows (above 64 handed back), top-p from 0.05 to
+    1, temperatures below and above 1, penalties below and above 1 over histories of 0-2499 ids
+    (above 2048 handed back), suppression ranges with a kept id, a banned id, and a fifth of the
+    rows rounded to integers (ties): ids against the oracle and the block path."""
+    rng = np.random.default_rng(9000 + seed)
+    rows = 2048
+    logits = (rng.standard_normal((rows, vocab)) * rng.choice([0.5, 2.0, 5.0], size=(rows, 1))).astype(np.float32)
+    tied = rng.random(rows) < 0.2
+    logits[tied] = np.round(logits[tied])
+    hl = rng.integers(0, 2500, size=rows)
+    off = np.zeros(rows + 1, np.int32)
+    off[1:] = np.cumsum(hl)
+    hist = rng.integers(0, vocab, size=off[-1]).astype(np.int32)
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = (rng.random(rows) > 0.05).astype(np.int32)
+    p["top_k"] = np.where(rng.random(rows) < 0.6, rng.integers(1, 81, rows), 0)
+    p["top_p"] = rng.choice([1.0, 0.95, 0.9, 0.5, 0.05], size=rows).astype(np.float32)
+    p["temperature"] = rng.choice([0.6, 0.9, 1.0, 1.4], size=rows).astype(np.float32)
+    p["rep_penalty"] = rng.choice([1.0, 1.05, 1.2, 0.9], size=rows).astype(np.float32)
+    supp = rng.random(rows) < 0.3
+    p["supp_begin"] = np.where(supp, rng.integers(0, vocab // 2, rows), 0)
+    p["supp_end"] = np.where(supp, vocab, 0)
+    p["keep_id"] = np.where(supp, vocab - 3, -1)
+    p["ban_id"] = np.where(rng.random(rows) < 0.1, 7, -1)
+    run_both_paths(ctx, logits, p, rng.random(rows), off, hist, label=f"random mix seed {seed} V {vocab}")
+
+
 @pytest.mark.parametrize("vocab", [300, 1000, 2048, 3072])
 def test_wave_top_k_edges(ctx, vocab):
     """Top-k on one wave at its edges: K = 1, 64 and 65 (the last handed back), logits quantised so
