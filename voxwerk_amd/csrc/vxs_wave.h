@@ -50,13 +50,14 @@ static_assert(kL == kWaveMaxTopK, "the one-wave top-k capacity is its lane count
 constexpr int kExact = 256;  // rows with at most this many candidates take the exact regime
 constexpr int kHP = 8;       // history ids per lane fetched with the row (512 per row)
 constexpr int kHMax = 2048;  // longest history the wave path takes (the rest in chunks of 8 per lane)
+constexpr int kDeadId = 1 << 14;  // history slot past the row's ids: above every vocabulary the path takes
 
 typedef double dbl2 __attribute__((ext_vector_type(2)));
 
 struct Sel {
     alignas(16) uint64_t hist[kNB];     // mass per bucket in units of 2^-F; then the draw's per-lane sweep sums
-    uint64_t key[kL + 4];   // crossing-bucket entries: mass bits << 32 | index, then 4 pads
-    uint64_t skey[kL];      // the same in rank order
+    uint32_t key[kL + 8];   // crossing-bucket entries (32-bit keys), then pads
+    uint32_t skey[kL];      // the same in rank order
     double ws[kL];          // their masses in rank order
     double stot;            // total mass, kept for the optional nucleus statistics
 };
@@ -146,7 +147,7 @@ __device__ __forceinline__ int wave_prepare(const SampleArgs& a, int r, int lane
 #pragma unroll
         for (int k = 0; k < kHP; k++) {
             const int h = w.h0 + lane + k * 64;
-            w.pre[k] = h < w.h1 ? a.hist_ids[h] : 0;
+            w.pre[k] = h < w.h1 ? a.hist_ids[h] : kDeadId;
         }
     }
     return 0;
@@ -257,28 +258,14 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
             if (lane == 0) a.out_ids[r] = VXS_ERR_ID_OUT_OF_RANGE;
             return 0;
         }
-#pragma unroll
-        for (int p0 = 0; p0 < NS; p0 += kPart) {
+        auto stage = [&](int p0) {
 #pragma unroll
             for (int c = 0; c < kPart; c++)
                 if (p0 + c < NS)
                     *(f4*)(xs + c * kSweep + lane4) =
                         f4{v[(p0 + c) * 4 + 0], v[(p0 + c) * 4 + 1], v[(p0 + c) * 4 + 2], v[(p0 + c) * 4 + 3]};
-            wsync();
-            const int lo = p0 * kSweep, span = (p0 + kPart < NS ? kPart : NS - p0) * kSweep;
-            {
-                int at[kHP];
-                float pv[kHP];
-#pragma unroll
-                for (int k = 0; k < kHP; k++) {
-                    const bool in = live[k] && (unsigned)(pre[k] - lo) < (unsigned)span;
-                    at[k] = in ? pre[k] - lo : kPart * kSweep + lane;
-                    pv[k] = penalize_fast(xs[at[k]], rho, rinv);
-                }
-#pragma unroll
-                for (int k = 0; k < kHP; k++) xs[at[k]] = pv[k];
-            }
-            wsync();
+        };
+        auto unstage = [&](int p0) {
 #pragma unroll
             for (int c = 0; c < kPart; c++)
                 if (p0 + c < NS) {
@@ -288,7 +275,64 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
                     v[(p0 + c) * 4 + 2] = q.z;
                     v[(p0 + c) * 4 + 3] = q.w;
                 }
-            wsync();  // the next part (or phase) overwrites the staging area
+        };
+        static_assert(NS <= 2 * kPart, "the penalty stages at most two parts");
+        if (NS <= kPart) {
+            // one part: every read of an original logit precedes every write of a penalised one;
+            // dead slots clamp to the dummy slot past the staged sweeps
+            uint32_t at[kHP];
+            float pv[kHP];
+            stage(0);
+            wsync();
+#pragma unroll
+            for (int k = 0; k < kHP; k++) {
+                at[k] = min((uint32_t)pre[k], (uint32_t)(kPart * kSweep));
+                pv[k] = penalize_fast(xs[at[k]], rho, rinv);
+            }
+#pragma unroll
+            for (int k = 0; k < kHP; k++) xs[at[k]] = pv[k];
+            wsync();
+            unstage(0);
+            wsync();
+        } else {
+            // Two parts of kPart sweeps. Each id's original logit is read while its part is staged
+            // (part 0, then part 1), its penalised value is computed once, and written back while
+            // its part is staged again (part 1 is still there; part 0 is staged a second time).
+            // Ids outside the staged part and dead slots clamp to the dummy slot kSpan.
+            constexpr uint32_t kSpan = kPart * kSweep;
+            uint32_t at0[kHP], at1[kHP];
+            float x0[kHP], xv[kHP];
+#pragma unroll
+            for (int k = 0; k < kHP; k++) {
+                at0[k] = min((uint32_t)pre[k], kSpan);
+                at1[k] = min((uint32_t)pre[k] - kSpan, kSpan);
+            }
+            stage(0);
+            wsync();
+#pragma unroll
+            for (int k = 0; k < kHP; k++) x0[k] = opaque(xs[at0[k]]);
+            wsync();
+            stage(kPart);
+            wsync();
+#pragma unroll
+            for (int k = 0; k < kHP; k++) {
+                const float x1 = opaque(xs[at1[k]]);  // both reads unconditional, then one select
+                xv[k] = (uint32_t)pre[k] >= kSpan ? x1 : x0[k];
+            }
+            float pv[kHP];
+#pragma unroll
+            for (int k = 0; k < kHP; k++) pv[k] = penalize_fast(xv[k], rho, rinv);
+#pragma unroll
+            for (int k = 0; k < kHP; k++) xs[at1[k]] = pv[k];
+            wsync();
+            unstage(kPart);
+            wsync();
+            stage(0);
+#pragma unroll
+            for (int k = 0; k < kHP; k++) xs[at0[k]] = pv[k];  // after the staging writes (same wave, in order)
+            wsync();
+            unstage(0);
+            wsync();  // the next phase overwrites the staging area
         }
         }
     }
@@ -490,7 +534,6 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
     if (cnt <= (uint32_t)kExact) return 1;  // exact regime beyond one wave
 
     // ================= nucleus regime =================
-    const double u = a.u ? a.u[r] : 0.0;
     const double thr = (double)(1.0f - P.top_p);
     const bool topp = P.top_p < 1.0f;
     if (topp && !(thr < 1.0)) return 1;  // top_p <= 0: every entry but the last in order goes
@@ -500,17 +543,9 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
     // 2^F and 2^-F built from their bits, so they stay in scalar registers
     const double gF = __longlong_as_double((long long)(1023 + F) << 52);
     const double gFi = __longlong_as_double((long long)(1023 - F) << 52);
-    // d = x - max replaces the logits (-inf stays -inf); the low byte of each d's bits is kept, one
-    // byte per entry (dl[c] byte j is entry 4c + j of the lane), to order entries of equal mass by d
-    uint32_t dl[NS];
+    // d = x - max replaces the logits (-inf stays -inf)
 #pragma unroll
     for (int e = 0; e < NE; e++) v[e] = v[e] - mx;
-#pragma unroll
-    for (int c = 0; c < NS; c++) {
-        const uint32_t lo01 = __builtin_amdgcn_perm(__float_as_uint(v[4 * c + 1]), __float_as_uint(v[4 * c]), 0x0c0c0400u);
-        const uint32_t lo23 = __builtin_amdgcn_perm(__float_as_uint(v[4 * c + 3]), __float_as_uint(v[4 * c + 2]), 0x0c0c0400u);
-        dl[c] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
-    }
     // masses replace d: nucleus_exp(d), on the 2^-F grid. When the smallest is at least 2^(23-F)
     // (and no entry is -inf) every mass is a multiple of 2^-F already and the rounding is skipped.
     const float qmin = mass_of(nucleus_exp(fmn - mx), Cb);
@@ -530,10 +565,10 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         const uint32_t base = (lb >> sh) & ~15u;
         const uint32_t pbase = (base + (uint32_t)(kBPL * lane)) & (kNB - 1);
         // Packed buckets when every mass is on the grid and a bucket lies inside one binade
-        // (sh <= 19: a lane's 16 buckets then share their exponent): each entry adds its count
-        // (high word) and its mantissa bits below the bucket's (low word, below 2^31 for 3072
-        // entries), from which the bucket's mass follows exactly. Otherwise each entry adds its
-        // mass in units of 2^-F.
+        // (sh <= 19: a lane's 16 buckets then share their exponent): each entry adds 2^40 (its
+        // count) plus its mass bits above its lane's smallest value (below 2^(sh+4), so below 2^35
+        // for 3072 entries), from which a bucket's or a lane's mass follows exactly. Otherwise each
+        // entry adds its mass in units of 2^-F.
         const bool packed = ongrid && sh <= 19;
 #pragma unroll
         for (int i = 0; i < kNB / 128; i++) *(dbl2*)&s.hist[(i * 64 + lane) * 2] = dbl2{0.0, 0.0};  // zero bits
@@ -541,14 +576,14 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         // the masses and their histogram atomics in one pass, so the atomics drain while the
         // remaining masses are computed
         if (packed) {
-            const uint32_t lmask = (1u << sh) - 1u;
+            const uint32_t lmask = (1u << (sh + 4)) - 1u;
 #pragma unroll
             for (int e = 0; e < NE; e++) {
                 const float q = nucleus_exp(v[e]);
                 v[e] = q;
                 const uint32_t qb = __float_as_uint(q);
                 atomicAdd((unsigned long long*)&s.hist[__builtin_amdgcn_ubfe(qb, (uint32_t)sh, 10u)],
-                          (unsigned long long)(qb & lmask) | (1ull << 32));
+                          (unsigned long long)(qb & lmask) | (1ull << 40));
             }
         } else {
             // Integer atomics (LDS adds u64 faster than f64): a mass below 2^(52-F) added to
@@ -567,11 +602,12 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
             }
         }
         wsync();
-        // mass of logical bucket (base + 16 * bl + j) in units of 2^-F from its packed entry
-        auto packed_units = [&](uint32_t bl, uint32_t j, uint64_t ent) -> uint64_t {
-            const uint32_t t = (base + 16u * bl + j) << sh;  // bits of the bucket's smallest value
+        // mass in units of 2^-F of packed entries (one bucket's, or a sum over buckets) of lane bl,
+        // whose values are (2^23 + mantissa of the lane's smallest) + offset, times 2^(exponent - 150)
+        auto packed_units = [&](uint32_t bl, uint64_t ent) -> uint64_t {
+            const uint32_t t = (base + 16u * bl) << sh;  // bits of the lane's smallest value
             const int sft = (int)(t >> 23) + F - 150;
-            const uint64_t m = (uint64_t)((t & 0x7fffffu) | 0x800000u) * (uint32_t)(ent >> 32) + (uint32_t)ent;
+            const uint64_t m = (uint64_t)((t & 0x7fffffu) | 0x800000u) * (ent >> 40) + (ent & ((1ull << 40) - 1));
             return sft >= 0 ? m << sft : 0ull;  // empty below the range
         };
         // lane totals in ascending bucket order, then the crossing lane, then the crossing bucket;
@@ -580,19 +616,10 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         uint64_t lti = 0;
         const int rot = (lane >> 1) & (kBPL - 1);
         if (packed) {
-            uint32_t N = 0, J = 0, Lo = 0;
+            uint64_t ent = 0;
 #pragma unroll
-            for (int j = 0; j < kBPL; j++) {
-                const uint64_t ent = s.hist[pbase + (j ^ rot)];
-                N += (uint32_t)(ent >> 32);
-                J += (uint32_t)(j ^ rot) * (uint32_t)(ent >> 32);
-                Lo += (uint32_t)ent;
-            }
-            // the 16 buckets share their exponent: sum of n_j * (M_0 + j * 2^sh) + low_j
-            const uint32_t t0 = (base + 16u * (uint32_t)lane) << sh;
-            const int sft = (int)(t0 >> 23) + F - 150;
-            const uint64_t m = (uint64_t)((t0 & 0x7fffffu) | 0x800000u) * N + Lo + ((uint64_t)J << sh);
-            lti = sft >= 0 ? m << sft : 0ull;
+            for (int j = 0; j < kBPL; j++) ent += s.hist[pbase + (j ^ rot)];
+            lti = packed_units((uint32_t)lane, ent);  // the 16 buckets share their exponent
         } else {
 #pragma unroll
             for (int j = 0; j < kBPL; j++) lti += s.hist[pbase + (j ^ rot)];
@@ -609,7 +636,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         const double runL = readlane_d(run, L);
         const uint32_t pL = (base + (uint32_t)(kBPL * L)) & (kNB - 1);
         const uint64_t hent = s.hist[pL + (lane & (kBPL - 1))];
-        const uint64_t hu = packed ? packed_units((uint32_t)L, (uint32_t)(lane & (kBPL - 1)), hent) : hent;
+        const uint64_t hu = packed ? packed_units((uint32_t)L, hent) : hent;
         const double hj = lane < kBPL ? (double)hu * gFi : 0.0;
         const double ij = row_incl_sum(hj);  // lanes 0..15 form one DPP row
         const double xj = runL + (ij - hj);
@@ -617,49 +644,53 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         if (!jb) return 1;
         const int jl = (int)__builtin_ctzll(jb);
         const double below = readlane_d(xj, jl);
-        const uint32_t glo = (base + (uint32_t)(kBPL * L + jl)) << sh;  // bits of the bucket's masses
+        uint32_t glo = (base + (uint32_t)(kBPL * L + jl)) << sh;  // bits of the bucket's masses
+        asm volatile("" : "+s"(glo));  // one subtraction per compare below
         const uint32_t gw = 1u << sh;
         // gather the crossing bucket (ballot compaction); the compares of a batch of eight slots
-        // are issued before their ballots are consumed
+        // are issued before their ballots are consumed. An entry's 32-bit key is its mass bits
+        // above the bucket's smallest (below 2^sh <= 2^19) shifted over its index (12 bits): key
+        // order is (mass, index) order inside the bucket.
+        if (sh > 19) return 1;
         uint32_t n = 0;
         uint32_t gwo = gw;
         asm volatile("" : "+s"(gwo));  // a plain unsigned compare (not rewritten into a shift and a test)
-        uint32_t* kw = reinterpret_cast<uint32_t*>(s.key);
+        uint32_t* kw = s.key;
 #pragma unroll
         for (int e0 = 0; e0 < NE; e0 += 8) {
             bool p[8];
+            uint32_t t[8];
             uint64_t bal[8];
 #pragma unroll
             for (int k = 0; k < 8; k++) {
-                p[k] = __float_as_uint(v[e0 + k]) - glo < gwo;
+                t[k] = __float_as_uint(v[e0 + k]) - glo;
+                p[k] = t[k] < gwo;
                 bal[k] = __ballot(p[k]);
             }
 #pragma unroll
             for (int k = 0; k < 8; k++) {
                 if (bal[k]) {
                     const uint32_t pos = n + mbcnt(bal[k]);
-                    if (p[k] && pos < (uint32_t)kL) {  // key: mass bits << 32 | index, as two words
-                        kw[2 * pos] = (uint32_t)eidx(e0 + k);
-                        kw[2 * pos + 1] = __float_as_uint(v[e0 + k]);
-                    }
+                    if (p[k] && pos < (uint32_t)kL) kw[pos] = (t[k] << 12) | (uint32_t)eidx(e0 + k);
                     n += (uint32_t)__builtin_popcountll(bal[k]);
                 }
             }
         }
         if (n > (uint32_t)kL) return 1;
-        if (lane < 4) s.key[n + lane] = ~0ull;
+        if (lane < 8) kw[n + lane] = ~0u;
         wsync();
         // rank by (mass, index): every lane compares its entry with all of them (broadcast reads)
         const int nn = (int)n;
-        const uint64_t ka = lane < nn ? s.key[lane] : ~0ull;
+        const uint32_t ka = lane < nn ? kw[lane] : ~0u;
         uint32_t rk = 0;
 #pragma unroll 1
-        for (int b = 0; b < nn; b += 4) {
-            const uint64_t* kp = &s.key[b];
+        for (int b = 0; b < nn; b += 8) {
+            const uint32_t* kp = &kw[b];
             rk += (kp[0] < ka) + (kp[1] < ka) + (kp[2] < ka) + (kp[3] < ka);
+            rk += (kp[4] < ka) + (kp[5] < ka) + (kp[6] < ka) + (kp[7] < ka);
         }
         if (lane < nn) {
-            s.ws[rk] = (double)__uint_as_float((uint32_t)(ka >> 32));
+            s.ws[rk] = (double)__uint_as_float(glo + (ka >> 12));
             s.skey[rk] = ka;
         }
         wsync();
@@ -668,55 +699,62 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         const uint64_t rb = __ballot(lane < nn && c0 <= T && T - c0 < w0);
         if (!rb) return 1;
         const int rl = (int)__builtin_ctzll(rb);
-        const uint32_t kc = (uint32_t)(s.skey[rl] >> 32);
+        const uint32_t kk = s.skey[rl];
+        const uint32_t kc = glo + (kk >> 12);
         qc = __uint_as_float(kc);
-        // The masses are a monotone function of d (nucleus_exp is monotone on gfx950 — checked
-        // over every float in [-128, 0] — and so is the rounding to the 2^-F grid), so (mass,
-        // index) order is the reference's (d, index) order except inside a group of equal masses,
-        // whose d may still differ: one rounding of d * log2 e can merge neighbouring values of d.
-        // A cut inside such a group removes the group's first rl - g0 members in (d, index) order.
-        // Where the mass is at most 1/2, equal masses imply d within a few ulps of each other, so
-        // the low bytes of their bits order them (modulo 256; larger bits, smaller d). Above 1/2
-        // (d within 0.7 of the max) a group can span many ulps: the general path takes the row.
-        if (rl > 0 && (uint32_t)(s.skey[rl - 1] >> 32) == kc) {
-            if (!(qc <= 0.5f)) return 1;
-            int g0 = rl - 1;
-            while (g0 > 0 && (uint32_t)(s.skey[g0 - 1] >> 32) == kc) g0--;
-            int g1 = rl + 1;
-            while (g1 < nn && (uint32_t)(s.skey[g1] >> 32) == kc) g1++;
-            // every member's low byte of d, fetched from the lane and register that hold it
-            const bool mem = lane >= g0 && lane < g1;
-            const uint32_t mi = mem ? (uint32_t)s.skey[lane] : 0u;
-            const int ol = (int)((mi >> 2) & 63u);
-            uint32_t word = 0;
+        // The masses are a monotone function of d (nucleus_exp is monotone on gfx950 — checked over
+        // every float in [-128, 0] — and so is the rounding to the 2^-F grid), so (mass, index)
+        // order is the reference's (d, index) order except inside a group of equal masses, whose d
+        // may differ (one rounding of d * log2 e can merge neighbouring values of d). When members
+        // of the cut's group rank before it (removed while the cut entry is kept), the group's d
+        // are recomputed from the caller's logits exactly as above: equal d order by index, as
+        // ranked here, and the removed members' masses are zeroed in their owner lanes. Unequal d
+        // (so the order is not known here): the general path takes the row.
+        if (rl > 0 && (s.skey[rl - 1] >> 12) == (kk >> 12)) {
+            if (h1 - h0 > kHP * 64) return 1;  // the history ids are not all in registers
+            const uint32_t kl = lane < nn ? s.skey[lane] : 0u;  // rank order
+            const bool grp = lane < nn && (kl >> 12) == (kk >> 12);
+            const int id = (int)(kl & 0xfffu);
+            // penalty membership of the members from an LDS bitmap of the history
+            typedef uint32_t u2w __attribute__((ext_vector_type(2)));
+            uint32_t* hbm = reinterpret_cast<uint32_t*>(s.hist);  // free after the scan: 4096 bits
+            *(u2w*)&hbm[2 * lane] = u2w{0u, 0u};
+            wsync();
+            if (pen_on) {  // the ids are read again (not kept in registers for this rare case)
 #pragma unroll
-            for (int c = 0; c < NS; c++) {
-                const uint32_t t = (uint32_t)__builtin_amdgcn_ds_bpermute(ol * 4, (int)dl[c]);
-                word = (int)(mi >> 8) == c ? t : word;
+                for (int k = 0; k < kHP; k++) {
+                    const int h = h0 + lane + 64 * k;
+                    if (h < h1) {
+                        const int hid = a.hist_ids[h];
+                        atomicOr(&hbm[hid >> 5], 1u << (hid & 31));
+                    }
+                }
             }
-            const uint32_t dlow = (word >> (8 * (mi & 3u))) & 0xffu;
-            const uint32_t ref = readlane(dlow, g0);
-            const int rel = (int)(int8_t)(uint8_t)(dlow - ref);  // larger: larger bits, smaller d
-            if (__ballot(mem && (rel > 32 || rel < -32))) return 1;
-            // order key: smaller d first, then smaller index
-            uint32_t* ok = reinterpret_cast<uint32_t*>(s.ws);
-            if (mem) ok[lane] = ((uint32_t)(127 - rel) << 16) | mi;
             wsync();
-            uint32_t grk = 0;
-            const uint32_t mine = mem ? ok[lane] : 0u;
-            for (int b = g0; b < g1; b++) grk += ok[b] < mine ? 1u : 0u;
-            const bool removed = mem && (int)grk < rl - g0;
-            // removed members' masses become 0: each sets its bit in its owner lane's mask
+            float d = 0.0f;
+            if (grp) {
+                float x = a.logits[(int64_t)r * a.ld + id];
+                if (pen_on && ((hbm[id >> 5] >> (id & 31)) & 1u)) {
+                    const float rho = P.rep_penalty;
+                    x = penalize_fast(x, rho, 1.0f / rho);
+                }
+                if (invT != 1.0f) x *= invT;
+                d = x - mx;
+            }
+            if (wave_fmin(grp ? d : kPosInf) != wave_fmax(grp ? d : kNegInf)) return 1;
+            // zero the removed members (ranks below rl): each sets its bit in its owner lane's mask
             wsync();
-            uint64_t* msk = reinterpret_cast<uint64_t*>(s.ws);
+            uint64_t* msk = reinterpret_cast<uint64_t*>(s.hist);
             msk[lane] = 0;
             wsync();
-            if (removed) atomicOr((unsigned long long*)&msk[ol], 1ull << ((mi >> 8) * 4 + (mi & 3u)));
+            if (grp && lane < rl)
+                atomicOr((unsigned long long*)&msk[(id >> 2) & 63], 1ull << ((id >> 8) * 4 + (id & 3)));
             wsync();
-            const uint64_t mm = msk[lane];
+            const uint64_t mz = msk[lane];
 #pragma unroll
             for (int e = 0; e < NE; e++)
-                if ((mm >> e) & 1ull) v[e] = 0.0f;
+                if ((mz >> e) & 1ull) v[e] = 0.0f;
+            wsync();  // the draw reuses the histogram area
         }
         Skept = S - readlane_d(c0, rl);
     } else {
@@ -738,6 +776,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
     // 2e-7, inside the 1e-6 band where a draw may differ from the reference's); sweep totals and
     // prefixes add those fp32 sums exactly in double precision, and the final walk recomputes the
     // same fp32 partial sums, so the lane found always holds the crossing.
+    const double u = a.u ? a.u[r] : 0.0;  // read here: a double live across the cut would spill
     const double D = floor(u * Skept * gF) * gFi;
     int pick;
     {
@@ -745,9 +784,9 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         float ls[NS];
 #pragma unroll
         for (int c = 0; c < NS; c++) {
-            float a = 0.0f;
+            float a = v[c * 4] >= qc ? v[c * 4] : 0.0f;  // masses are >= +0, so 0 + a would be a
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
+            for (int j = 1; j < 4; j++) {
                 const float q = v[c * 4 + j];
                 a += q >= qc ? q : 0.0f;
             }
@@ -773,29 +812,39 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         const uint64_t sb = __ballot((lane & 3) == 0 && sc < NS && D < xi);
         if (!sb) return 1;  // no crossing (rounding at the top of the range): general path
         const int sl = (int)__builtin_ctzll(sb);
-        const int cs = sl >> 2;
+        const int cs = __builtin_amdgcn_readfirstlane(sl >> 2);
         const double before = readlane_d(xi, sl) - readlane_d(x, sl);
-        float mine = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NS; c++)
-            if (c == cs) mine = ls[c];
+        // sweep cs's partial sum and masses: a uniform switch (register arrays indexed by a
+        // runtime value would go to scratch)
+        float mine = 0.0f, q4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        switch (cs) {
+#define VXS_SWEEP(C)                                                                   \
+    case C:                                                                            \
+        if constexpr (C < NS) {                                                        \
+            mine = ls[C];                                                              \
+            q4[0] = v[C * 4]; q4[1] = v[C * 4 + 1]; q4[2] = v[C * 4 + 2]; q4[3] = v[C * 4 + 3]; \
+        }                                                                              \
+        break;
+            VXS_SWEEP(0) VXS_SWEEP(1) VXS_SWEEP(2) VXS_SWEEP(3) VXS_SWEEP(4) VXS_SWEEP(5)
+            VXS_SWEEP(6) VXS_SWEEP(7) VXS_SWEEP(8) VXS_SWEEP(9) VXS_SWEEP(10) VXS_SWEEP(11)
+#undef VXS_SWEEP
+            default: break;
+        }
+        static_assert(NS <= 12, "the switch covers 12 sweeps");
         const double md = (double)mine;
         const double li = before + wave_incl_sum(md);
         const uint64_t lb2 = __ballot(D < li);
         if (!lb2) return 1;
         const int L2 = (int)__builtin_ctzll(lb2);
         pick = -1;
+        {
+            const double b0 = li - md;
+            float a = 0.0f;
 #pragma unroll
-        for (int c = 0; c < NS; c++) {
-            if (c == cs) {
-                const double b0 = li - md;
-                float a = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float q = opaque(v[c * 4 + j]);
-                    a += q >= qc ? q : 0.0f;
-                    pick = (pick < 0 && D < b0 + (double)a) ? eidx(c * 4 + j) : pick;
-                }
+            for (int j = 0; j < 4; j++) {
+                const float q = q4[j];
+                a += q >= qc ? q : 0.0f;
+                pick = (pick < 0 && D < b0 + (double)a) ? cs * kSweep + lane * 4 + j : pick;
             }
         }
         pick = (int)readlane((uint32_t)pick, L2);
