@@ -63,6 +63,10 @@ struct SampleArgs {
     int32_t* done_count;
     int32_t* done_flag;
     int32_t done_seq;
+    // One-wave kernel launch stagger (set by its launcher): workgroups from stagger_from on start
+    // their loads after stagger_sleeps x 2048 cycles of s_sleep.
+    int stagger_from;
+    int stagger_sleeps;
 };
 
 enum : int {

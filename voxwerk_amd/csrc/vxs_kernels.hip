@@ -1412,17 +1412,15 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void sa
     const int lane = threadIdx.x & 63;
     const int r0 = blockIdx.x * kWaves;
     const int r = r0 + wv;
-    // Staggered halves: workgroups reach the CUs in index order, about 256 per round (one per CU),
-    // and a 4096-row batch puts four rounds on every CU, one wave of each per SIMD. The second
-    // half of the batch (two waves per SIMD) starts its loads about 2.6 us (3 x 2048 cycles of
-    // s_sleep) after the first and runs at a lower wave priority, so the first half's rows arrive
-    // first and compute, two waves per SIMD, while the second half loads. 4096 x 3072: 22.0 ->
-    // 21.0 us. Tried: priority alone 21.7 us; four rounds 1.7 us apart 21.3 us (2.6 us apart 22.4);
-    // rounds from the wave's slot on its SIMD instead of the workgroup index: the same.
-    {
-        const uint32_t half = blockIdx.x >> 9;
-        if (half == 0) __builtin_amdgcn_s_setprio(3);
-        for (uint32_t i = 0; i < 3u * min(half, 1u); i++) __builtin_amdgcn_s_sleep(32);
+    // Staggered halves (launch_quad sets the split): when the whole grid is resident at once (at
+    // most four workgroups per CU, one wave of each per SIMD), the second half of the workgroups
+    // starts its loads after a delay proportional to the first half's bytes and runs at a lower
+    // wave priority, so the first half's rows arrive first and compute while the second half loads.
+    // Larger grids run in several rounds, which stagger by themselves, and take no delay.
+    if (a.stagger_sleeps) {
+        const bool late = (int)blockIdx.x >= a.stagger_from;
+        if (!late) __builtin_amdgcn_s_setprio(3);
+        for (int i = 0; late && i < a.stagger_sleeps; i++) __builtin_amdgcn_s_sleep(32);
     }
     int b = 0;
     if (r < a.rows) b = wave_fast_row<NS, kStats>(a, vec, r, lane, sm.wave[wv]);
@@ -1445,9 +1443,35 @@ hipError_t launch_nc(const SampleArgs& a, int vec, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// Compute units of the current device (cached per device).
+int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
 template <int NS, int NC>
-hipError_t launch_quad(const SampleArgs& a, int vec, hipStream_t stream) {
+hipError_t launch_quad(const SampleArgs& a_in, int vec, hipStream_t stream) {
+    SampleArgs a = a_in;
     const dim3 grid((a.rows + kWaves - 1) / kWaves);
+    // The stagger of sample_quad_kernel: a grid resident in one round with three or four
+    // workgroups per CU delays its second half by about 2.6 us per full round of 4 x CUs
+    // workgroups (3 x 2048 cycles of s_sleep at 4096 rows on 256 CUs). Measured, 3072-entry
+    // rows, staggered / not: 2049 rows (none) 15.6 us, 3072 rows 18.27 / 18.52, 4096 rows 21.04 /
+    // 21.60; 6144 and 8192 rows run in two rounds and take none.
+    const int g = (int)grid.x, cus = device_cus();
+    a.stagger_from = g;
+    a.stagger_sleeps = 0;
+    if (g <= 4 * cus && g >= 3 * cus) {
+        a.stagger_from = g / 2;
+        a.stagger_sleeps = (3 * g + 2 * cus) / (4 * cus);
+    }
     if (a.out_stats)  // a separate instance, so the statistics cost the sampling kernel nothing
         hipLaunchKernelGGL((sample_quad_kernel<NS, NC, true>), grid, dim3(kT), 0, stream, a, vec);
     else
