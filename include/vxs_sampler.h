@@ -138,8 +138,9 @@ VXS_API int vxs_sample_device(vxs_ctx* ctx, int rows, int vocab, const float* d_
  * the caller's memory into a fixed 16 MiB device scratch (one per GPU, held until the process ends),
  * the kernels read them there and write the ids there, and the ids are copied back. A call that
  * needs more than the scratch (about rows * vocab * 4 bytes plus the histories, params and
- * uniforms) fails with VXS_ERR_UNSUPPORTED. Every context on one GPU shares that GPU's scratch:
- * calls that overlap on one GPU (from several threads or contexts) race; serialise them.
+ * uniforms) fails with VXS_ERR_UNSUPPORTED. Every context on one GPU shares that GPU's scratch, so
+ * the library serialises the calls on one GPU (from any threads or contexts) with a per-device lock
+ * held for the whole call: concurrent calls wait for each other.
  */
 VXS_API int vxs_sample_noalloc(vxs_ctx* ctx, int rows, int vocab, const float* logits, int64_t ld,
                                const int32_t* hist_off, const int32_t* hist_ids, const vxs_params* params,

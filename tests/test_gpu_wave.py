@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 from oracle import ref
-from parity import compare_ids
+from parity import compare_ids, signed_zero_batch
 from voxwerk_amd import workloads
 from voxwerk_amd._lib import PARAMS_DTYPE
 
@@ -263,3 +263,54 @@ def test_wave_long_histories(ctx):
     for r in bad_rows:
         if hl[r] > 600:
             assert wave[r] == -2, (r, wave[r])  # VXS_ERR_ID_OUT_OF_RANGE
+
+
+def test_wave_signed_zero_at_kth(ctx):
+    """+0 and -0 at the k-th value: the forced wave path on 96 rows and the default path on a full
+    1024-row batch (which takes the one-wave kernel), against the oracle and the block path."""
+    rng = np.random.default_rng(4242)
+    x, p, u, off, hist = signed_zero_batch(rng, 96, 3072)
+    wave, _ = run_both_paths(ctx, x, p, u, off, hist, label="signed zeros (wave)")
+    assert (wave >= 0).all()
+    assert (x[np.arange(0, 96, 3), wave[::3]] == 0.0).all()  # K = 1 rows draw one of the zeros
+    x, p, u, off, hist = signed_zero_batch(rng, 1024, 3072)
+    ids = ctx.sample(x, p, u, off, hist, raise_on_error=False)
+    block = ctx.sample(x, p, u, off, hist, path="block", raise_on_error=False)
+    rep = compare_ids(ids, ref.sample(x, p, u, off, hist, threads=8))
+    print(f"signed zeros (1024 rows): {rep}", flush=True)
+    assert not rep.unexplained, f"ids differ at rows {rep.unexplained[:10]}"
+    assert np.array_equal(ids, block)
+
+
+def test_wave_top_k_at_tiny_penalised_logits(ctx):
+    """Positive logits below 2^-60 in the history (penalised by rho 1.1 or 0.9) next to entries one
+    ulp either side of their quotients and a maximum of 1, with the k-th largest value among the
+    tiny ones: the k-th value and the kept set depend on the quotients being correctly rounded."""
+    rng = np.random.default_rng(977)
+    rows, vocab = 64, 3072
+    x = rng.uniform(-9.0, -1.0, (rows, vocab)).astype(np.float32)
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = 1
+    p["top_p"] = 1.0
+    p["temperature"] = 1.0
+    p["keep_id"], p["ban_id"] = -1, -1
+    off = np.zeros(rows + 1, np.int32)
+    hist = []
+    for r in range(rows):
+        rho = np.float32(1.1 if r % 2 == 0 else 0.9)
+        p["rep_penalty"][r] = rho
+        pos = rng.permutation(vocab)
+        n = 12
+        t = (np.float32(2.0 ** -70) * rng.uniform(1.0, 2.0 ** 9, n)).astype(np.float32)  # 2^-70 .. 2^-61
+        x[r, pos[:n]] = t
+        q = (t / rho).astype(np.float32)  # the correctly rounded penalised values
+        up = np.nextafter(q, np.float32(1.0))
+        dn = np.nextafter(q, np.float32(0.0))
+        x[r, pos[n:2 * n]] = np.where(rng.random(n) < 0.5, up, dn)
+        x[r, pos[2 * n:3 * n]] = q
+        x[r, pos[3 * n]] = 1.0  # the maximum, well above 2^-30
+        hist.append(pos[:n].astype(np.int32))
+        off[r + 1] = off[r] + n
+        p["top_k"][r] = int(rng.integers(2, 3 * n + 1))
+    u = rng.random(rows)
+    run_both_paths(ctx, x, p, u, off, np.concatenate(hist), label="tiny penalised logits at the k-th value")

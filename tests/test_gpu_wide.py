@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 from oracle import ref
-from parity import PROB_RTOL, comparable_rows, compare_ids, prob_rel_error
+from parity import PROB_RTOL, comparable_rows, compare_ids, prob_rel_error, signed_zero_batch
 from voxwerk_amd import workloads
 from voxwerk_amd._lib import PARAMS_DTYPE
 
@@ -179,3 +179,12 @@ def test_wide_handback_next_to_ordered_rows(ctx):
             x[r, cols[:300]] = np.float32(x[r].max() + 0.5)  # 300 ties at the k-th value
             x[r, cols[300:350]] = np.float32(x[r].max() + 2.0)
     check_rows(ctx, x, b.params, b.u, b.hist_off, b.hist_ids, label="wide hand-back mix")
+
+
+def test_wide_signed_zero_at_kth(ctx):
+    """+0 and -0 at the k-th value of 151936-entry rows (K = 1 over zeros, ties of zeros after a few
+    positive entries), with write-back logits and probabilities against the oracle."""
+    x, p, u, off, hist = signed_zero_batch(np.random.default_rng(5151), 24, 151936)
+    ids, _ = check_rows(ctx, x, p, u, off, hist, label="wide signed zeros")
+    assert (ids >= 0).all()
+    assert (x[np.arange(0, 24, 3), ids[::3]] == 0.0).all()

@@ -2,7 +2,8 @@
 device scratch) against vxs_sample on the same inputs, through the C ABI: ids identical, on two
 calls in a row, the second smaller (a different shape, histories whose offsets do not start at 0,
 a leading dimension above the vocabulary, strided params), then a call too large for the scratch,
-which must fail cleanly and leave the next call working."""
+which must fail cleanly and leave the next call working; a wide-vocabulary call (the streaming
+kernel), and two contexts calling from two threads at once."""
 import numpy as np
 import pytest
 
@@ -89,3 +90,70 @@ def test_noalloc_rejects_calls_beyond_the_scratch(ctx):
     ids = np.full(3, -99, np.int32)
     rc = ctx._lib.vxs_sample_noalloc(ctx.handle, 3, vocab, ptr(small), vocab, None, None, ptr(p), 0, None, ptr(ids), 0)
     assert rc == 0 and (ids == 7).all()
+
+
+def test_noalloc_wide_vocabulary(ctx):
+    """16 rows of the 151936-entry workload with 4096-id histories (about 9.8 MB staged): the
+    streaming kernel reading its inputs from the fixed scratch."""
+    w = workloads.workload(5)
+    b = w.generate(rows=16)
+    print(f"noalloc wide call: {b.rows} x {w.vocab}", flush=True)
+    rc0, want = reference(ctx, b.logits, w.vocab, b.params, 1, b.u, b.hist_off, b.hist_ids)
+    ids = np.full(b.rows, -99, np.int32)
+    rc = ctx._lib.vxs_sample_noalloc(ctx.handle, b.rows, w.vocab, ptr(b.logits), w.vocab, ptr(b.hist_off),
+                                     ptr(b.hist_ids), ptr(b.params), 1, ptr(b.u), ptr(ids), 0)
+    assert rc == rc0 == 0, ctx.last_error()
+    assert np.array_equal(ids, want)
+
+
+def test_noalloc_two_contexts_two_threads(ctx):
+    """Two contexts on one GPU calling from two threads at once, with inputs of different shapes:
+    the per-device lock keeps the calls from overlapping in the shared scratch, so every call
+    returns vxs_sample's ids."""
+    import threading
+
+    from voxwerk_amd.sampler import Context
+
+    rng = np.random.default_rng(99)
+    jobs = []
+    for rows, vocab in ((512, 3072), (300, 2000)):
+        x = (rng.standard_normal((rows, vocab)) * 2.0).astype(np.float32)
+        off = (np.arange(rows + 1) * 30).astype(np.int32)
+        hist = rng.integers(0, vocab, off[-1]).astype(np.int32)
+        p = np.zeros(rows, dtype=PARAMS_DTYPE)
+        p["do_sample"] = 1
+        p["top_p"] = np.float32(0.9)
+        p["temperature"] = np.float32(0.8)
+        p["rep_penalty"] = np.float32(1.1)
+        p["keep_id"], p["ban_id"] = -1, -1
+        u = rng.random(rows)
+        rc, want = reference(ctx, x, vocab, p, 1, u, off, hist)
+        assert rc == 0
+        jobs.append((x, vocab, off, hist, p, u, want))
+    other = Context(0)
+    calls = 40
+    bad = []
+    start = threading.Barrier(2)
+
+    def run(c, job, tag):
+        x, vocab, off, hist, p, u, want = job
+        start.wait()
+        for i in range(calls):
+            ids = np.full(x.shape[0], -99, np.int32)
+            rc = c._lib.vxs_sample_noalloc(c.handle, x.shape[0], vocab, ptr(x), vocab, ptr(off), ptr(hist), ptr(p), 1,
+                                           ptr(u), ptr(ids), 0)
+            if rc != 0 or not np.array_equal(ids, want):
+                bad.append((tag, i, rc))
+
+    print(f"noalloc two threads: {calls} calls each", flush=True)
+    try:
+        ts = [threading.Thread(target=run, args=(c, j, t)) for c, j, t in ((ctx, jobs[0], "a"), (other, jobs[1], "b"))]
+        for t in ts:
+            t.start()
+        for t in ts:
+            t.join(timeout=100)
+        assert not any(t.is_alive() for t in ts), "a thread did not finish"
+    finally:
+        if not any(t.is_alive() for t in ts):
+            other.close()
+    assert not bad, bad[:5]

@@ -632,6 +632,8 @@ VXS_API int vxs_sample_noalloc(vxs_ctx* ctx, int rows, int vocab, const float* l
             return fail(ctx, VXS_ERR_UNSUPPORTED,
                         "vxs_sample_noalloc: this call stages " + std::to_string(need) + " bytes; the fixed scratch holds " +
                             std::to_string(vxs::kNoAllocScratchBytes));
+        // one call at a time per device: the scratch is the device's, not the context's
+        std::lock_guard<std::mutex> hold(vxs::noalloc_lock(ctx->device));
         VXS_HIP(ctx, hipSetDevice(ctx->device));
         char* d = static_cast<char*>(ctx->noalloc);
         hipStream_t st = ctx->stream;

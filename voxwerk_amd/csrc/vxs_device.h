@@ -767,12 +767,12 @@ __device__ __forceinline__ float penalize(float s, float rho, float rinv, bool f
     return __builtin_fmaf(rem, rinv, t0);
 }
 
-// The same penalty without branches for the common case: s*rho for s < 0, else the Markstein
+// The same penalty without branches for the common case: s*rho for s <= 0, else the Markstein
 // quotient, which is the correctly rounded s/rho unless penalize_needs_division(s, fast).
 __device__ __forceinline__ float penalize_fast(float s, float rho, float rinv) {
     const float t0 = s * rinv;
     const float q = __builtin_fmaf(__builtin_fmaf(-t0, rho, s), rinv, t0);
-    return s < 0.0f ? s * rho : q;
+    return s <= 0.0f ? s * rho : q;  // zeros keep their sign, as s / rho keeps it
 }
 __device__ __forceinline__ bool penalize_needs_division(float s, bool fast) {
     return !(s < 0.0f) && !(fast && s >= 0x1p-60f && s <= 0x1p60f);

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/vxs_sampler.h"
 
 namespace vxs {
@@ -227,6 +229,8 @@ hipError_t launch_frame_embed(const FrameEmbedArgs& a, hipStream_t stream);
 // `device`, which must be the current device (looked up once per device, then cached).
 constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
 hipError_t noalloc_scratch(int device, void** out);
+// The lock a call holds while it uses `device`'s scratch (device as accepted by noalloc_scratch).
+std::mutex& noalloc_lock(int device);
 
 // Enqueue the sampler on `stream`. Returns hipSuccess or the launch error.
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream);

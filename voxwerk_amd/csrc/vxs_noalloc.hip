@@ -5,7 +5,9 @@
 // stages them in this array instead: a file-scope device array of kNoAllocScratchBytes, one copy
 // per GPU, held until the process ends. Host code never passes the array's name to a kernel or a
 // copy (in host code it only stands for the symbol): set-up looks up its device address once per
-// device, with that device current, and every use goes through that address.
+// device, with that device current, and every use goes through that address. A per-device lock,
+// held by vxs_sample_noalloc for the whole (synchronous) call, keeps calls on one GPU from
+// overlapping in its scratch, whichever threads or contexts make them.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -20,6 +22,7 @@ __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 void* g_ptr[kMaxDevices] = {};
+std::mutex g_use[kMaxDevices];  // held while a call stages, samples and fetches on that device
 
 }  // namespace
 
@@ -40,5 +43,7 @@ hipError_t noalloc_scratch(int device, void** out) {
     *out = g_ptr[device];
     return hipSuccess;
 }
+
+std::mutex& noalloc_lock(int device) { return g_use[device]; }
 
 }  // namespace vxs

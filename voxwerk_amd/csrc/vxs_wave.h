@@ -178,11 +178,12 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
     // reads and writes are unmasked: an id outside the part uses the lane's own spare slot.
     // The quotient is the Markstein-corrected one (penalize_fast): correctly rounded for rho with
     // |rho| in [2^-20, 2^20] (other rows go to the general path) and logits in [2^-60, 2^60] or
-    // negative. The rest cannot change the sampled id here: -0 becomes +0, which gives the same d
-    // and mass and compares equal; a positive logit below 2^-60, off by at most 2^-83, gives the
-    // same d = fl32(x - max) when the maximum is at least 2^-30, and a row whose maximum lies in
-    // (0, 2^-30) or at or above 2^100 (or is not finite) goes to the general path after the
-    // statistics below.
+    // not positive (zeros keep their sign). A positive logit below 2^-60 becomes a value below
+    // 2^-40 that may be off by at most 2^-83. That cannot change the sampled id: it gives the same
+    // d = fl32(x - max) when the maximum is at least 2^-30 (a row whose maximum lies in (0, 2^-30)
+    // or at or above 2^100, or is not finite, goes to the general path after the statistics
+    // below), and a top-k row whose k-th largest value lies in [0, 2^-39), the only place such an
+    // entry could fall on the wrong side of the k-th value, goes to the general path there.
     if (pen_on && h1 > h0) {
         const float rho = P.rep_penalty;
         const float arho = __builtin_fabsf(rho);
@@ -504,6 +505,8 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
                 if (c >= K) lo = mid;
                 else hi = mid - 1;
             }
+            // the k-th value near a penalised positive logit below 2^-60 (see S1)
+            if (pen_on && h1 > h0 && lo >= f2key(0.0f) && lo < f2key(0x1p-39f)) return 1;
             // the final candidates (>= the k-th largest), still in index order
             nf = 0;
 #pragma unroll
