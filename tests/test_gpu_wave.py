@@ -314,3 +314,40 @@ def test_wave_top_k_at_tiny_penalised_logits(ctx):
         p["top_k"][r] = int(rng.integers(2, 3 * n + 1))
     u = rng.random(rows)
     run_both_paths(ctx, x, p, u, off, np.concatenate(hist), label="tiny penalised logits at the k-th value")
+
+
+def test_wave_handback_rows_take_one_wave_exact_in_turn(ctx):
+    """Every row of the batch handed back by the one-wave kernel (more than 256 entries at or above
+    the K-th largest lane maximum: five lanes hold only large values), yet with 50 candidates after
+    top-k, so each of a workgroup's four rows in turn reaches the one-wave exact regime of the
+    one-workgroup algorithm (one wave samples while the others wait for the next row): ids against
+    the oracle and the block path."""
+    rng = np.random.default_rng(5050)
+    rows, vocab = 1024, 3072
+    lane_of = (np.arange(vocab) % 256) // 4  # lane l holds entries c * 256 + 4 l + j
+    x = rng.uniform(-3.0, 0.0, (rows, vocab)).astype(np.float32)
+    hist = []
+    off = np.zeros(rows + 1, np.int32)
+    for r in range(rows):
+        hot = rng.choice(64, 5, replace=False)
+        hot_e = np.isin(lane_of, hot)
+        x[r, hot_e] = rng.uniform(5.0, 6.0, hot_e.sum()).astype(np.float32)
+        for l in np.setdiff1d(np.arange(64), hot):
+            e = rng.choice(np.flatnonzero(lane_of == l))
+            x[r, e] = np.float32(rng.uniform(4.0, 4.99))
+        lane_max = np.array([x[r, lane_of == l].max() for l in range(64)])
+        tf = np.sort(lane_max)[::-1][49]
+        assert (x[r] >= tf).sum() > 256  # the one-wave gather overflows: handed back
+        h = rng.choice(np.flatnonzero(~hot_e), 40, replace=False).astype(np.int32)
+        hist.append(h)
+        off[r + 1] = off[r] + len(h)
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = 1
+    p["top_k"] = 50
+    p["top_p"] = rng.choice([1.0, 0.9], size=rows).astype(np.float32)
+    p["temperature"] = np.float32(0.9)
+    p["rep_penalty"] = np.float32(1.05)
+    p["keep_id"], p["ban_id"] = -1, -1
+    u = rng.random(rows)
+    wave, _ = run_both_paths(ctx, x, p, u, off, np.concatenate(hist), label="handed-back top-k rows")
+    assert (wave >= 0).all()

@@ -1,10 +1,14 @@
 // vxs_latency.cpp — host-to-host latency of vxs_sample through the C ABI, timed in native code (the
 // way a P/Invoke caller sees it: host logits in, host id out, no interpreter in between).
 //
-// usage: vxs_latency <input file> <iterations>
+// usage: vxs_latency <input file> <iterations> [steps]
 // input file (little-endian): int32 rows, int32 vocab, int32 hist_len, then rows*vocab float32 logits,
 // rows*hist_len int32 history ids, rows vxs_params, rows float64 uniforms.
-// output: one JSON line {"p50_us": .., "p99_us": .., "iters": .., "id0": ..}
+// With `steps` S > 1 the rows are S consecutive blocks of rows / S, one call each in order (the
+// dependent steps of a frame, e.g. the 15 code-predictor stages of TalkerGenerator.cs:262-269), and
+// an iteration is one frame of S calls.
+// output: one JSON line {"p50_us": .., "p99_us": .., "iters": .., "id0": ..} per call, plus
+// "frame_p50_us", "frame_p99_us", "steps" when S > 1.
 //
 // usage: vxs_latency --binding-frame <frames> [writeback]
 // One frame of single-sequence generation (TalkerGenerator.Generate, TalkerGenerator.cs:241-272) as the
@@ -198,7 +202,7 @@ int main(int argc, char** argv) {
         return frame_mode(rows, iters, argc >= 5 && std::strcmp(argv[4], "serial") == 0);
     }
     if (argc < 3) {
-        std::fprintf(stderr, "usage: %s <input file> <iterations> | --frame <rows> <iterations> [serial] | --binding-frame <frames> "
+        std::fprintf(stderr, "usage: %s <input file> <iterations> [steps] | --frame <rows> <iterations> [serial] | --binding-frame <frames> "
                      "[writeback]\n", argv[0]);
         return 2;
     }
@@ -227,36 +231,57 @@ int main(int argc, char** argv) {
     }
     for (int r = 0; r <= rows; r++) off[r] = r * hlen;
     const int iters = std::max(1, std::atoi(argv[2]));
+    const int steps = argc >= 4 ? std::atoi(argv[3]) : 1;
+    if (steps <= 0 || rows % steps) {
+        std::fprintf(stderr, "steps must divide the rows\n");
+        return 2;
+    }
+    const int rs = rows / steps;  // rows per call
 
     vxs_ctx* ctx = nullptr;
-    if (vxs_create(&ctx, 0, rows, vocab, (int64_t)rows * hlen) != VXS_OK) {
+    if (vxs_create(&ctx, 0, rs, vocab, (int64_t)rs * hlen) != VXS_OK) {
         std::fprintf(stderr, "vxs_create failed\n");
         return 1;
     }
-    auto call = [&]() {
-        return vxs_sample(ctx, rows, vocab, logits.data(), vocab, hlen ? off.data() : nullptr,
-                          hlen ? hist.data() : nullptr, params.data(), 1, u.data(), ids.data(), nullptr, nullptr, 0);
+    // call k: rows [k * rs, (k + 1) * rs); the offsets index the whole history array
+    auto call = [&](int k) {
+        const size_t r0 = (size_t)k * rs;
+        return vxs_sample(ctx, rs, vocab, logits.data() + r0 * vocab, vocab, hlen ? off.data() + r0 : nullptr,
+                          hlen ? hist.data() : nullptr, params.data() + r0, 1, u.data() + r0, ids.data() + r0, nullptr,
+                          nullptr, 0);
     };
     for (int i = 0; i < 200; i++)
-        if (call() != VXS_OK) {
+        if (call(i % steps) != VXS_OK) {
             std::fprintf(stderr, "vxs_sample failed: %s\n", vxs_last_error(ctx));
             vxs_destroy(ctx);
             return 1;
         }
-    std::vector<double> t(iters);
+    std::vector<double> t((size_t)iters * steps), fr(iters);
     for (int i = 0; i < iters; i++) {
-        const auto a = std::chrono::steady_clock::now();
-        const int rc = call();
-        t[i] = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - a).count();
-        if (rc != VXS_OK) {
-            std::fprintf(stderr, "vxs_sample failed: %s\n", vxs_last_error(ctx));
-            vxs_destroy(ctx);
-            return 1;
+        const auto f0 = std::chrono::steady_clock::now();
+        for (int k = 0; k < steps; k++) {
+            const auto a = std::chrono::steady_clock::now();
+            const int rc = call(k);
+            t[(size_t)i * steps + k] = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - a).count();
+            if (rc != VXS_OK) {
+                std::fprintf(stderr, "vxs_sample failed: %s\n", vxs_last_error(ctx));
+                vxs_destroy(ctx);
+                return 1;
+            }
         }
+        fr[i] = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - f0).count();
     }
     vxs_destroy(ctx);
     std::sort(t.begin(), t.end());
-    std::printf("{\"p50_us\": %.2f, \"p99_us\": %.2f, \"iters\": %d, \"id0\": %d}\n", t[iters / 2],
-                t[(size_t)(iters * 0.99)], iters, ids[0]);
+    std::sort(fr.begin(), fr.end());
+    const size_t n = t.size();
+    if (steps == 1) {
+        std::printf("{\"p50_us\": %.2f, \"p99_us\": %.2f, \"iters\": %d, \"id0\": %d}\n", t[n / 2],
+                    t[(size_t)(n * 0.99)], iters, ids[0]);
+    } else {
+        std::printf("{\"p50_us\": %.2f, \"p99_us\": %.2f, \"iters\": %zu, \"steps\": %d, \"frame_p50_us\": %.2f, "
+                    "\"frame_p99_us\": %.2f, \"frames\": %d, \"id0\": %d}\n",
+                    t[n / 2], t[(size_t)(n * 0.99)], n, steps, fr[iters / 2], fr[(size_t)(iters * 0.99)], iters, ids[0]);
+    }
     return 0;
 }
