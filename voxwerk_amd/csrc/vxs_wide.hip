@@ -932,13 +932,12 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
     const float* __restrict__ xrow = a.logits + (int64_t)r * a.ld;
     const float invT = row_inv_temp(P);
     const int K = P.top_k;
-    {
-        // HW_ID: SIMD_ID in bits 5:4, the workgroup's slot on its CU in bits 19:16. The wave whose
-        // SIMD equals the slot runs this row's sequential tail, so the tails of the workgroups
-        // sharing a CU land on different SIMDs (checked below: exactly one such wave, else wave 0).
-        const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
-        if (g.lane == 0) s.wslot[g.wv] = ((hw >> 4) & 3u) == ((hw >> 16) & 3u) ? 1 : 0;
-    }
+    // HW_ID: SIMD_ID in bits 5:4, the workgroup's slot on its CU in bits 19:16. The wave whose
+    // SIMD equals the slot runs this row's sequential tail, so the tails of the workgroups sharing a
+    // CU land on different SIMDs (checked below: exactly one such wave, else wave 0).
+    const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+    const uint32_t slot = (hw >> 16) & 3u;
+    if (g.lane == 0) s.wslot[g.wv] = ((hw >> 4) & 3u) == slot ? 1 : 0;
 
     // the wave ranges and the row loads (the first sweeps are in flight while the bitmap is built)
     const int Q = ((V + kTW * 4 - 1) / (kTW * 4)) * 256;  // a wave's range, a multiple of 256
@@ -1095,6 +1094,18 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
     // (loads past the row return zeros, so they are issued unconditionally)
     {
         for (int gb = lo; gb < hi; gb += kPF * 256) {
+            // The workgroups sharing a CU take turns at the highest wave priority, about 10 us
+            // each (s_memrealtime counts at 100 MHz): with equal priorities the oldest workgroup's
+            // loads issue first and the rows finish pass A in order of age, 90 to 112 us into the
+            // wide workload's step, so the last rows' tails end the step; in turns the rows finish
+            // it together (99 to 108 us) and the step takes 129 instead of 132 us.
+            {
+                const uint32_t turn = ((uint32_t)(__builtin_amdgcn_s_memrealtime() >> 10) + slot) & 3u;
+                if (turn == 0) __builtin_amdgcn_s_setprio(0);
+                else if (turn == 1) __builtin_amdgcn_s_setprio(1);
+                else if (turn == 2) __builtin_amdgcn_s_setprio(2);
+                else __builtin_amdgcn_s_setprio(3);
+            }
             // another wave may have raised the shared bound: use it too
             const uint32_t ts = __hip_atomic_load(&s.tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             f4 nxt[kPF];
