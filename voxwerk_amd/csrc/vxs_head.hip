@@ -3,10 +3,11 @@
 // CodecHead and CodePredictorHead (src/Voxwerk/Talker/TalkerModel.cs:133-137) multiply a few fp32
 // hidden rows by a bf16 weight (the checkpoint's [out, in] layout, WeightPrecision.BFloat16,
 // DecoderStack.cs:7-15): out[r][n] = sum_k x[r][k] * W[n][k]. With the rows of a decode step
-// (1-24) this is a GEMV bound by reading W once from HBM; the products stay fp32 (no MFMA, which
-// would round x to bf16), and the logits stay in HBM for the sampler.
+// (1-24) this is a GEMV; the logits stay in HBM for the sampler. From 8 rows the matrix cores take it
+// (head_mfma_kernel, with x split exactly into three bf16 parts); below, the VALU form with fp32
+// products.
 //
-// Layout: a wave owns R = 8 consecutive outputs (4 when k > 1024, 2 for one or two rows); lane l
+// VALU layout: a wave owns R = 8 consecutive outputs (4 when k > 1024, 2 for one or two rows); lane l
 // holds W[n][k] for k = 512 j + 8 l + 0..7
 // (one 16-byte load per output and j, 1 KiB contiguous per wave instruction), all of its rows in
 // registers for the whole call. Per hidden row the lane loads its x slice (the next row's loads
@@ -27,6 +28,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "vxs_internal.h"
 
@@ -247,6 +249,162 @@ __global__ __launch_bounds__(kHT) void head_i8_kernel(HeadArgs a) {
     }
 }
 
+// ---- matrix-core form, for 8 or more rows -------------------------------------------------------
+// The hidden rows are fp32 and v_mfma_f32_16x16x32_bf16 multiplies bf16, so each x is split exactly
+// into three bf16 parts, x = h + m + l: h keeps the top 8 significand bits (truncation), m the next
+// 8 of the remainder x - h (exact in fp32), l what is left (at most 8 bits: exact in bf16), exact
+// whenever |x| >= 2^-110 or x = 0. A bf16 weight times a part is exact in fp32, so the matrix cores
+// sum exact products: out = W h + W m + W l, with fp32 roundings only in the accumulation (a chain
+// of at most 3 K / 32 + 2 matrix operations and NW wave partials per output; the test bound is that
+// of K sequential fp32 additions). An int8 weight widens to bf16 exactly (|q| <= 127).
+//
+// Tile: a workgroup owns 16 TM outputs and all rows, 32 at a time; its NW waves split K in chunks
+// of 64 (two 32-deep steps), chunk c to wave c % NW, and their 16 TM x 32 partial sums are added in
+// LDS in wave order. MFMA operand layout (16x16x32): lane l supplies A[l % 16][8 (l / 16) + 0..7] and
+// B[8 (l / 16) + 0..7][l % 16], and holds C[4 (l / 16) + i][l % 16], i = 0..3. Here A = W (outputs by
+// k), B = x^T (k by rows), so lane l reads 8 consecutive k of one weight row and of one hidden row.
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+
+// three exact bf16 parts of 8 fp32 values
+__device__ __forceinline__ void split3(const f4& a, const f4& b, bf8& h, bf8& m, bf8& l) {
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t th[8], tm[8], tl[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        th[i] = __float_as_uint(v[i]) & 0xFFFF0000u;
+        const float r1 = v[i] - __uint_as_float(th[i]);
+        tm[i] = __float_as_uint(r1) & 0xFFFF0000u;
+        tl[i] = __float_as_uint(r1 - __uint_as_float(tm[i]));
+    }
+    u4 ph, pm, pl;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {  // high halves of elements 2i (low) and 2i + 1 (high)
+        ph[i] = __builtin_amdgcn_perm(th[2 * i + 1], th[2 * i], 0x07060302u);
+        pm[i] = __builtin_amdgcn_perm(tm[2 * i + 1], tm[2 * i], 0x07060302u);
+        pl[i] = __builtin_amdgcn_perm(tl[2 * i + 1], tl[2 * i], 0x07060302u);
+    }
+    h = __builtin_bit_cast(bf8, ph);
+    m = __builtin_bit_cast(bf8, pm);
+    l = __builtin_bit_cast(bf8, pl);
+}
+
+// 8 int8 weights (two dwords) as 8 bf16: the biased byte converted, 128 subtracted (exact), the
+// high halves packed
+__device__ __forceinline__ bf8 i8_to_bf16(uint32_t lo, uint32_t hi) {
+    lo ^= 0x80808080u;
+    hi ^= 0x80808080u;
+    uint32_t f[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        f[i] = __float_as_uint((float)(((i < 4 ? lo : hi) >> (8 * (i & 3))) & 0xffu) - 128.0f);
+    u4 p;
+#pragma unroll
+    for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_perm(f[2 * i + 1], f[2 * i], 0x07060302u);
+    return __builtin_bit_cast(bf8, p);
+}
+
+template <int TM, int NW, bool I8>
+__global__ __launch_bounds__(64 * NW) void head_mfma_kernel(HeadArgs a) {
+    __shared__ f4 part[NW][TM * 2][64];  // each wave's accumulators, per (output tile, row tile)
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int n0 = blockIdx.x * 16 * TM;
+    const int nchunks = (a.k + 63) / 64;
+    for (int r0 = 0; r0 < a.rows; r0 += 32) {
+        f4 acc[TM][2];
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+            for (int tn = 0; tn < 2; tn++) acc[tm][tn] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int c = wv; c < nchunks; c += NW) {
+            // every load of the chunk is issued before the first product: the weights of both steps
+            // and output tiles, the hidden rows' slices of both steps and row tiles (lane l: 8
+            // consecutive k from 64 c + 32 step + 8 (l / 16), weight row / hidden row l % 16 of the tile)
+            typedef typename std::conditional<I8, u2, u4>::type WRaw;
+            WRaw wr[2][TM];
+            f4 xr[2][2][2];
+            bool kin[2];
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                const int k = 64 * c + 32 * st + 8 * g;  // k % 8 == 0: the 8 are all inside or all past k
+                kin[st] = k < a.k;
+#pragma unroll
+                for (int tm = 0; tm < TM; tm++) {
+                    const int n = n0 + 16 * tm + c16;
+                    const int64_t off = (int64_t)min(n, a.n - 1) * a.ldw + (kin[st] ? k : 0);
+                    if constexpr (I8)
+                        wr[st][tm] = *reinterpret_cast<const u2*>(a.q + off);
+                    else
+                        wr[st][tm] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(a.w + off));
+                }
+#pragma unroll
+                for (int tn = 0; tn < 2; tn++) {
+                    const int r = r0 + 16 * tn + c16;
+                    const float* px = a.x + (int64_t)min(r, a.rows - 1) * a.ldx + (kin[st] ? k : 0);
+                    xr[st][tn][0] = *reinterpret_cast<const f4*>(px);
+                    xr[st][tn][1] = *reinterpret_cast<const f4*>(px + 4);
+                }
+            }
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                bf8 wa[TM];
+#pragma unroll
+                for (int tm = 0; tm < TM; tm++) {
+                    const bool in = kin[st] && n0 + 16 * tm + c16 < a.n;
+                    if constexpr (I8)
+                        wa[tm] = i8_to_bf16(in ? wr[st][tm].x : 0u, in ? wr[st][tm].y : 0u);
+                    else
+                        wa[tm] = __builtin_bit_cast(bf8, in ? wr[st][tm] : u4{0u, 0u, 0u, 0u});
+                }
+#pragma unroll
+                for (int tn = 0; tn < 2; tn++) {
+                    const bool in = kin[st] && r0 + 16 * tn + c16 < a.rows;
+                    const f4 z = {0.f, 0.f, 0.f, 0.f};
+                    bf8 h, m, l;
+                    split3(in ? xr[st][tn][0] : z, in ? xr[st][tn][1] : z, h, m, l);
+#pragma unroll
+                    for (int tm = 0; tm < TM; tm++) {
+                        acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[tm], h, acc[tm][tn], 0, 0, 0);
+                        acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[tm], m, acc[tm][tn], 0, 0, 0);
+                        acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[tm], l, acc[tm][tn], 0, 0, 0);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+            for (int tn = 0; tn < 2; tn++) part[wv][2 * tm + tn][lane] = acc[tm][tn];
+        __syncthreads();
+        // (output, row) pairs of the tile, consecutive threads on consecutive outputs: the waves'
+        // partials added in wave order, scaled (int8), stored
+        for (int p = threadIdx.x; p < 16 * TM * 32; p += 64 * NW) {
+            const int nl = p % (16 * TM), rl = p / (16 * TM);
+            const int tm = nl / 16, mi = nl % 16, tn = rl / 16;
+            const int l = 16 * (mi / 4) + rl % 16;
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) sum += part[w][2 * tm + tn][l][mi % 4];
+            const int n = n0 + nl, r = r0 + rl;
+            if (n < a.n && r < a.rows) {
+                if constexpr (I8) sum *= a.scale[n];
+                a.out[(int64_t)r * a.ldo + n] = sum;
+            }
+        }
+        __syncthreads();  // the partials are read before the next row group writes them
+    }
+}
+
+template <int TM, int NW>
+hipError_t launch_mfma(const HeadArgs& a, hipStream_t stream) {
+    const dim3 grid((a.n + 16 * TM - 1) / (16 * TM));
+    if (a.q)
+        hipLaunchKernelGGL((head_mfma_kernel<TM, NW, true>), grid, dim3(64 * NW), 0, stream, a);
+    else
+        hipLaunchKernelGGL((head_mfma_kernel<TM, NW, false>), grid, dim3(64 * NW), 0, stream, a);
+    return hipGetLastError();
+}
+
 // FromBf16LinearInt8 for one output row per workgroup.
 __global__ __launch_bounds__(kHT) void head_pack_i8_kernel(int k, const uint16_t* __restrict__ w, int64_t ldw,
                                                           int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale) {
@@ -299,6 +457,7 @@ hipError_t launch_kr(HeadArgs a, hipStream_t stream) {
 
 hipError_t launch_head(const HeadArgs& a, hipStream_t stream) {
     if (a.rows <= 0 || a.n <= 0) return hipSuccess;
+    if (a.rows >= 8 && a.k >= 64) return launch_mfma<1, 16>(a, stream);
     // Outputs per wave: eight up to k = 1024 (four above, for registers); with one or two rows, two,
     // so that the single pass over the weight is spread over four times as many waves.
     const bool few = a.rows <= 2;
