@@ -227,3 +227,37 @@ def test_step_on_device_int8_head_sampler(ctx):
     ids = d_ids.numpy()
     c = ref.classify(ids, ref.sample(logits, p, u))
     assert c["unexplained"] == 0, c
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_head_nonfinite_hidden_values(ctx, int8):
+    """Matrix-core form (8 or more rows): +inf, -inf and NaN in the hidden rows give what IEEE
+    products and sums give (the classes of the float64 results: +-inf, NaN), finite rows stay
+    within the bound."""
+    rng = np.random.default_rng(17)
+    rows, k, n = 12, 1024, 256
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    x[1, 5] = np.inf
+    x[3, 100] = -np.inf
+    x[5, 7] = np.nan
+    x[7, 9], x[7, 10] = np.inf, -np.inf
+    wf = rng.standard_normal((n, k)) * 0.05
+    wf[:8, 5] = 0.0  # inf times a zero weight: NaN
+    w = _bf16(wf)
+    if int8:
+        q, scale = _pack_on_gpu(ctx, w)
+        got = _run_int8(ctx, x, q, scale)
+        wd = q.astype(np.float64)
+    else:
+        got = _run(ctx, x, w)
+        wd = (w.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    want = np.empty((rows, n))
+    with np.errstate(invalid="ignore"):
+        for r in range(rows):  # elementwise products and a plain sum: IEEE classes, no library shortcuts
+            want[r] = (x[r].astype(np.float64)[:, None] * wd.T).sum(axis=0)
+    for r in (1, 3, 5, 7):
+        assert np.array_equal(np.isnan(got[r]), np.isnan(want[r])), r
+        assert np.array_equal(np.isposinf(got[r]), np.isposinf(want[r])), r
+        assert np.array_equal(np.isneginf(got[r]), np.isneginf(want[r])), r
+    fin = [0, 2, 4, 6, 8, 9, 10, 11]
+    assert np.all(np.isfinite(got[fin]))

@@ -265,14 +265,25 @@ __global__ __launch_bounds__(kHT) void head_i8_kernel(HeadArgs a) {
 // k), B = x^T (k by rows), so lane l reads 8 consecutive k of one weight row and of one hidden row.
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 
-// three exact bf16 parts of 8 fp32 values
+// three exact bf16 parts of 8 fp32 values. With NONFINITE, +-inf and NaN are their own high part (a
+// NaN keeps a payload bit in the bf16 half) with zero remainders, so the products follow IEEE
+// (inf w = +-inf, inf 0 = NaN, NaN w = NaN); without it such a value would turn into NaN parts.
+template <bool NONFINITE>
 __device__ __forceinline__ void split3(const f4& a, const f4& b, bf8& h, bf8& m, bf8& l) {
     const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     uint32_t th[8], tm[8], tl[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        th[i] = __float_as_uint(v[i]) & 0xFFFF0000u;
-        const float r1 = v[i] - __uint_as_float(th[i]);
+        const uint32_t u = __float_as_uint(v[i]);
+        float r1;
+        if constexpr (NONFINITE) {
+            const bool fin = (u & 0x7F800000u) != 0x7F800000u;
+            th[i] = fin || !(u & 0x007FFFFFu) ? u & 0xFFFF0000u : u | 0x00400000u;
+            r1 = fin ? v[i] - __uint_as_float(th[i]) : 0.0f;
+        } else {
+            th[i] = u & 0xFFFF0000u;
+            r1 = v[i] - __uint_as_float(th[i]);
+        }
         tm[i] = __float_as_uint(r1) & 0xFFFF0000u;
         tl[i] = __float_as_uint(r1 - __uint_as_float(tm[i]));
     }
@@ -286,6 +297,19 @@ __device__ __forceinline__ void split3(const f4& a, const f4& b, bf8& h, bf8& m,
     h = __builtin_bit_cast(bf8, ph);
     m = __builtin_bit_cast(bf8, pm);
     l = __builtin_bit_cast(bf8, pl);
+}
+
+// split3 with the non-finite handling only when the wave holds such a value (one class test per
+// value; the rare case takes the longer form)
+__device__ __forceinline__ void split3_any(const f4& a, const f4& b, bf8& h, bf8& m, bf8& l) {
+    bool nf = false;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        nf |= __builtin_amdgcn_class(a[i], 0x207) | __builtin_amdgcn_class(b[i], 0x207);  // NaN, +-inf
+    if (__ballot(nf))
+        split3<true>(a, b, h, m, l);
+    else
+        split3<false>(a, b, h, m, l);
 }
 
 // 8 int8 weights (two dwords) as 8 bf16: the biased byte converted, 128 subtracted (exact), the
@@ -361,7 +385,7 @@ __global__ __launch_bounds__(64 * NW) void head_mfma_kernel(HeadArgs a) {
                     const bool in = kin[st] && r0 + 16 * tn + c16 < a.rows;
                     const f4 z = {0.f, 0.f, 0.f, 0.f};
                     bf8 h, m, l;
-                    split3(in ? xr[st][tn][0] : z, in ? xr[st][tn][1] : z, h, m, l);
+                    split3_any(in ? xr[st][tn][0] : z, in ? xr[st][tn][1] : z, h, m, l);
 #pragma unroll
                     for (int tm = 0; tm < TM; tm++) {
                         acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[tm], h, acc[tm][tn], 0, 0, 0);
