@@ -365,6 +365,14 @@ int stage_and_launch(vxs_ctx* ctx, int rows, int vocab, const float* logits, int
         a.done_seq = done->done_seq;
     }
     if (res) set_resident(a, res->store, reinterpret_cast<const int32_t*>(d + L.hoff), res->append, res->rng_stream);
+    if (zero_copy && rows == 1 && !res && a.path == vxs::kPathBlock) {
+        // one row read in place over PCIe: its scalars travel in the kernel arguments
+        a.row_direct = 1;
+        a.direct_params = params[0];
+        a.direct_h0 = 0;
+        a.direct_h1 = hist_off ? hoff[1] : 0;
+        a.direct_u = u ? u[0] : 0.0;
+    }
     VXS_HIP(ctx, vxs::launch_sample(a, ctx->stream));
     return VXS_OK;
 }

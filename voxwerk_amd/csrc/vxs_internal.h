@@ -69,6 +69,13 @@ struct SampleArgs {
     // their loads after stagger_sleeps x 2048 cycles of s_sleep.
     int stagger_from;
     int stagger_sleeps;
+    // A single-row host call's scalars by value (row_direct = 1, one-workgroup kernel): the options,
+    // the history range and the uniform, so the kernel reads none of them from host memory over
+    // PCIe before its history ids (or at the draw).
+    int row_direct;
+    int direct_h0, direct_h1;
+    double direct_u;
+    vxs_params direct_params;
 };
 
 enum : int {
@@ -95,6 +102,7 @@ struct HistRange {
     int h0, h1;
 };
 __device__ __forceinline__ HistRange history_range(const SampleArgs& a, int r) {
+    if (a.row_direct) return {a.direct_h0, a.direct_h1};
     if (!a.hist_len) return {a.hist_off[r], a.hist_off[r + 1]};
     const int s = a.hist_slot[r];
     const bool ok = (unsigned)s < (unsigned)a.hist_slots;
@@ -146,6 +154,7 @@ __device__ __forceinline__ double row_uniform(const SampleArgs& a, int r) {
         if ((unsigned)s >= (unsigned)d.slots) return 0.0;
         return rng_double(rng_peek(slot_rng(a, d, s)).v);
     }
+    if (a.row_direct) return a.direct_u;
     return a.u ? a.u[r] : 0.0;
 }
 

@@ -540,7 +540,11 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
             for (int j = 0; j < 4; j++) v[c * 4 + j] = xrow[min(i0 + j, V - 1)];
         }
     }
-    const vxs_params P = a.params[(int64_t)r * a.params_stride];
+    vxs_params P;
+    if (a.row_direct)
+        P = a.direct_params;
+    else
+        P = a.params[(int64_t)r * a.params_stride];
     HistRange hr{0, 0};
     if (has_history(a)) hr = history_range(a, r);
     const bool pen_on = P.rep_penalty != 1.0f && has_history(a);
