@@ -41,7 +41,8 @@ def _run(ctx, x, w, ldx=None, ldw=None, ldo=None):
     return out[:, :n]
 
 
-@pytest.mark.parametrize("rows,k,n", [(1, 1024, 3072), (24, 1024, 2048), (5, 1024, 3001)])
+@pytest.mark.parametrize("rows,k,n", [(1, 1024, 3072), (24, 1024, 2048), (5, 1024, 3001), (24, 1024, 3072),
+                                      (8, 2048, 2560), (32, 64, 4099)])
 def test_head_exact_on_integers(ctx, rows, k, n):
     rng = np.random.default_rng(rows + n)
     x = rng.integers(-8, 9, (rows, k)).astype(np.float32)
@@ -53,7 +54,7 @@ def test_head_exact_on_integers(ctx, rows, k, n):
 @pytest.mark.parametrize("rows,k,n,pad", [(24, 1024, 3072, 0), (1, 1024, 2048, 0), (64, 1024, 3072, 8),
                                           (3, 200, 100, 0), (7, 776, 1000, 16), (9, 1536, 513, 0),
                                           (2, 2048, 3072, 0), (4, 8, 7, 0), (2, 1024, 5, 0), (1, 1536, 3001, 8),
-                                          (1, 512, 64, 0)])
+                                          (1, 512, 64, 0), (32, 776, 3001, 16), (9, 1536, 2560, 8), (17, 64, 4096, 0)])
 def test_head_within_fp32_bound(ctx, rows, k, n, pad):
     rng = np.random.default_rng(rows * 1000 + k + n)
     x = rng.standard_normal((rows, k)).astype(np.float32)
@@ -161,7 +162,7 @@ def test_pack_int8_bit_exact(ctx, n, k, ldw, ldq):
 
 
 @pytest.mark.parametrize("rows,k,n,scale", [(1, 1024, 3072, 1.0), (24, 1024, 2048, 0.5), (5, 1024, 3001, 0.25),
-                                            (3, 2048, 100, 1.0)])
+                                            (3, 2048, 100, 1.0), (24, 1024, 3072, 0.5), (32, 1536, 2560, 2.0)])
 def test_head_int8_exact_on_integers(ctx, rows, k, n, scale):
     """Small integers and a power-of-two scale: every partial sum and the scaling are exact."""
     rng = np.random.default_rng(rows * 7 + n)
@@ -175,7 +176,7 @@ def test_head_int8_exact_on_integers(ctx, rows, k, n, scale):
 
 @pytest.mark.parametrize("rows,k,n,pad", [(24, 1024, 3072, 0), (1, 1024, 2048, 0), (64, 1024, 3072, 8),
                                           (3, 200, 100, 0), (7, 776, 1000, 16), (9, 1536, 513, 0),
-                                          (2, 2048, 3072, 0), (4, 8, 7, 0), (1, 1536, 3001, 8)])
+                                          (2, 2048, 3072, 0), (4, 8, 7, 0), (1, 1536, 3001, 8), (16, 776, 3001, 16)])
 def test_head_int8_within_bound(ctx, rows, k, n, pad):
     """Weights packed on the GPU, then the head: within gamma_{K+1} * scale * sum|x q| of the exact
     value, the bound both reference forms (decode and batched) satisfy."""
@@ -231,11 +232,10 @@ def test_step_on_device_int8_head_sampler(ctx):
 
 @pytest.mark.parametrize("int8", [False, True])
 def test_head_nonfinite_hidden_values(ctx, int8):
-    """Matrix-core form (8 or more rows): +inf, -inf and NaN in the hidden rows give what IEEE
-    products and sums give (the classes of the float64 results: +-inf, NaN), finite rows stay
-    within the bound."""
+    """Matrix-core form (8 to 32 rows, 2560 outputs or more): +inf, -inf and NaN in the hidden rows
+    give what IEEE products and sums give (the classes of the float64 results: +-inf, NaN)."""
     rng = np.random.default_rng(17)
-    rows, k, n = 12, 1024, 256
+    rows, k, n = 12, 1024, 2560
     x = rng.standard_normal((rows, k)).astype(np.float32)
     x[1, 5] = np.inf
     x[3, 100] = -np.inf

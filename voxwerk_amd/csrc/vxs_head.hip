@@ -481,7 +481,11 @@ hipError_t launch_kr(HeadArgs a, hipStream_t stream) {
 
 hipError_t launch_head(const HeadArgs& a, hipStream_t stream) {
     if (a.rows <= 0 || a.n <= 0) return hipSuccess;
-    if (a.rows >= 8 && a.k >= 64) return launch_mfma<1, 16>(a, stream);
+    // The matrix-core form for 8 to 32 rows and at least 2560 outputs (160 or more workgroups of
+    // 16 outputs). Measured, 24 rows x 1024, matrix cores / VALU: 3072 outputs 6.8 / 7.9 us, 2048
+    // outputs 6.8 / 6.4 us; 8 rows x 3072 5.4 / 6.1 us; 64 rows (two row groups in turn) 13.4 /
+    // 12.6 us at 3072 outputs and 13.3 / 9.4 us at 2048.
+    if (a.rows >= 8 && a.rows <= 32 && a.n >= 2560 && a.k >= 64) return launch_mfma<1, 16>(a, stream);
     // Outputs per wave: eight up to k = 1024 (four above, for registers); with one or two rows, two,
     // so that the single pass over the weight is spread over four times as many waves.
     const bool few = a.rows <= 2;
