@@ -36,7 +36,7 @@ extern "C" {
 #define VXS_ERR_ID_OUT_OF_RANGE (-2) /* history id < 0 or >= vocab (C#: Span indexer at Sampler.cs:30)   */
 #define VXS_ERR_NONFINITE (-3)       /* NaN or +inf logit after temperature: outside the contract        */
 #define VXS_ERR_HIP (-4)             /* HIP runtime failure; text in vxs_last_error                      */
-#define VXS_ERR_UNSUPPORTED (-5)     /* shape outside what this build implements; text in vxs_last_error */
+#define VXS_ERR_UNSUPPORTED (-5)     /* shape outside what the library implements; text in vxs_last_error */
 #define VXS_ERR_NO_DEVICE (-6)       /* no usable gfx950 device                                          */
 #define VXS_ERR_HISTORY_FULL (-7)    /* resident history slot already holds `cap` ids (vxs_sample_batch)  */
 
