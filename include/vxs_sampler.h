@@ -156,11 +156,14 @@ VXS_API int vxs_sample_noalloc(vxs_ctx* ctx, int rows, int vocab, const float* l
  *   d_stats[4r + 3] = 0,
  * so that the nucleus is checked beyond the id; all four are NaN for every other row (greedy,
  * exact regime, rows the one-workgroup algorithm samples). d_stats is [rows][4] fp64 device memory.
+ * d_probs (optional, [rows][vocab] fp64 device memory): for the same rows, every entry's final
+ * probability as the draw used it (its mass over the kept mass, 0 for removed entries); NaN for
+ * every other row.
  */
 VXS_API int vxs_sample_stats_device(vxs_ctx* ctx, int rows, int vocab, const float* d_logits, int64_t ld,
                                     const int32_t* d_hist_off, const int32_t* d_hist_ids,
                                     const vxs_params* d_params, int params_stride, const double* d_u,
-                                    int32_t* d_out_ids, double* d_stats, uint32_t flags);
+                                    int32_t* d_out_ids, double* d_stats, double* d_probs, uint32_t flags);
 
 /* Wait for all work queued on the context stream. */
 VXS_API int vxs_synchronize(vxs_ctx* ctx);

@@ -134,3 +134,59 @@ def test_equal_mass_cut_nucleus(ctx):
             x[r, group[::2]] = base
             p["top_p"][r] = rng.choice([0.4, 0.6, 0.7])
     check_stats(ctx, x, p, rng.random(rows), label="equal-mass cuts", min_wave_rows=rows // 2)
+
+
+def _per_entry(ctx, logits, params, u, off, hist, label):
+    from voxwerk_amd.hip import DeviceArray
+
+    rows, vocab = logits.shape
+    d = [DeviceArray.from_numpy(np.ascontiguousarray(a)) for a in (logits, params, np.asarray(u, np.float64))]
+    d_off = DeviceArray.from_numpy(off) if off is not None else None
+    d_hist = DeviceArray.from_numpy(hist) if hist is not None else None
+    d_ids, d_stats = DeviceArray((rows,), np.int32), DeviceArray((rows, 4), np.float64)
+    d_probs = DeviceArray((rows, vocab), np.float64)
+    ctx.sample_stats_device(rows, vocab, d[0], vocab, d[1], 1, d[2], d_ids, d_stats, d_off, d_hist, path="wave",
+                            probs=d_probs)
+    ctx.synchronize()
+    ids, st, pr = d_ids.numpy(), d_stats.numpy(), d_probs.numpy()
+    ora = ref.sample(logits, params, u, off, hist, threads=8, want_probs=True)
+    wave = st[:, 3] == 0
+    assert np.isnan(pr[~wave]).all(), f"{label}: probabilities written for rows outside the one-wave nucleus"
+    ok = wave & comparable_rows(ids, ora)
+    po, pk = ora["probs"][ok], pr[ok]
+    # masses live on a 2^-F grid of exp(d) (F = 41 at 3072 entries): an entry whose exp(d) is below
+    # half a step gets mass 0, and one near the grid's step carries its rounding; above 2^-41 * 1e5
+    # every probability agrees within 1e-5 relative, and every one within one step absolute
+    F = min(51, 53 - int(np.ceil(np.log2(vocab))))
+    big = po >= 2.0 ** -F * 1e5
+    rel = np.abs(pk[big] - po[big]) / po[big]
+    assert rel.max(initial=0.0) <= 1e-5, f"{label}: probability rel error {rel.max():.3e}"
+    assert np.all(np.abs(pk - po) <= 2.0 ** -F + 1e-5 * po), f"{label}: probability abs error"
+    assert np.all(((pk > 0) == (po > 0)) | (po < 2.0 ** -F)), f"{label}: kept sets differ"
+    print(f"{label}: {int(ok.sum())} rows, {int(big.sum())} probabilities, max rel err {rel.max(initial=0.0):.2e}, "
+          f"{int(((pk == 0) & (po > 0)).sum())} below the grid", flush=True)
+
+
+def test_per_entry_probabilities_headline(ctx):
+    """Every entry's final probability from the one-wave nucleus kernel (the timed kernel's stats
+    build) against the oracle's, on the first 1024 rows of the headline batch."""
+    w = workloads.workload(4)
+    b = w.generate(rows=1024)
+    _per_entry(ctx, b.logits, b.params, b.u, b.hist_off, b.hist_ids, w.name)
+
+
+def test_per_entry_probabilities_option_mix(ctx):
+    rng = np.random.default_rng(4711)
+    rows, vocab = 512, 3072
+    logits = (rng.standard_normal((rows, vocab)) * rng.choice([0.5, 2.0, 4.0], size=(rows, 1))).astype(np.float32)
+    hl = rng.integers(0, 300, size=rows)
+    off = np.zeros(rows + 1, np.int32)
+    off[1:] = np.cumsum(hl)
+    hist = rng.integers(0, vocab, size=off[-1]).astype(np.int32)
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = 1
+    p["top_p"] = rng.choice([1.0, 0.99, 0.95, 0.8, 0.5], size=rows).astype(np.float32)
+    p["temperature"] = rng.choice([0.7, 1.0, 1.3], size=rows).astype(np.float32)
+    p["rep_penalty"] = rng.choice([1.0, 1.05, 1.3], size=rows).astype(np.float32)
+    p["keep_id"], p["ban_id"] = -1, -1
+    _per_entry(ctx, logits, p, rng.random(rows), off, hist, "per-entry option mix")

@@ -92,7 +92,7 @@ _SIGNATURES = {
     "vxs_sample_device": (c_int, [c_void_p, c_int, c_int, _P, c_int64, _P, _P, _P, c_int, _P, _P, _P, _P, c_uint32]),
     "vxs_sample_noalloc": (c_int, [c_void_p, c_int, c_int, _P, c_int64, _P, _P, _P, c_int, _P, _P, c_uint32]),
     "vxs_sample_stats_device": (c_int, [c_void_p, c_int, c_int, _P, c_int64, _P, _P, _P, c_int, _P, _P, _P,
-                                        c_uint32]),
+                                        _P, c_uint32]),
     "vxs_synchronize": (c_int, [c_void_p]),
     "vxs_apply_repetition_penalty": (c_int, [c_void_p, c_int, c_int, _P, c_int64, _P, _P, c_float]),
     "vxs_argmax": (c_int, [c_void_p, c_int, c_int, _P, c_int64, _P]),

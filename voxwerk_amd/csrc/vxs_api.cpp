@@ -733,7 +733,7 @@ VXS_API int vxs_sample_device(vxs_ctx* ctx, int rows, int vocab, const float* d_
 VXS_API int vxs_sample_stats_device(vxs_ctx* ctx, int rows, int vocab, const float* d_logits, int64_t ld,
                                     const int32_t* d_hist_off, const int32_t* d_hist_ids, const vxs_params* d_params,
                                     int params_stride, const double* d_u, int32_t* d_out_ids, double* d_stats,
-                                    uint32_t flags) {
+                                    double* d_probs, uint32_t flags) {
     try {
         int rc = check_shape(ctx, rows, vocab, d_logits, ld, d_params, params_stride, d_out_ids);
         if (rc != VXS_OK) return rc;
@@ -745,6 +745,7 @@ VXS_API int vxs_sample_stats_device(vxs_ctx* ctx, int rows, int vocab, const flo
         VXS_HIP(ctx, hipSetDevice(ctx->device));
         // all-ones bytes: every double NaN, for the rows the one-wave nucleus regime does not sample
         VXS_HIP(ctx, hipMemsetAsync(d_stats, 0xff, sizeof(double) * 4 * (size_t)rows, ctx->stream));
+        if (d_probs) VXS_HIP(ctx, hipMemsetAsync(d_probs, 0xff, sizeof(double) * (size_t)rows * vocab, ctx->stream));
         vxs::SampleArgs a{};
         a.rows = rows;
         a.vocab = vocab;
@@ -757,6 +758,7 @@ VXS_API int vxs_sample_stats_device(vxs_ctx* ctx, int rows, int vocab, const flo
         a.u = d_u;
         a.out_ids = d_out_ids;
         a.out_stats = d_stats;
+        a.out_stat_probs = d_probs;
         a.kflags = 0;
         a.path = choose_path(flags, rows, vocab);
         VXS_HIP(ctx, vxs::launch_sample(a, ctx->stream));

@@ -56,6 +56,9 @@ struct SampleArgs {
     // Optional [rows][4] (parity/debug): for a row the one-wave nucleus regime samples, its kept
     // fraction of the mass, smallest kept probability, kept count and 0; other rows are untouched.
     double* out_stats;
+    // Optional [rows][vocab] with out_stats: for the same rows, every entry's final probability
+    // (its mass over the kept mass; 0 for removed entries).
+    double* out_stat_probs;
     uint32_t kflags;
     int path;            // kPathBlock or kPathQuad
     // Host-visible completion for small host calls (one workgroup per row): after its row, every

@@ -873,6 +873,14 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
             o[2] = (double)kn;
             o[3] = 0.0;
         }
+        if (a.out_stat_probs) {  // the probabilities the draw used: kept masses over the kept mass
+            double* pr = a.out_stat_probs + (int64_t)r * a.vocab;
+#pragma unroll
+            for (int e = 0; e < NE; e++) {
+                const int i = (e >> 2) * kSweep + lane * 4 + (e & 3);
+                if (i < a.vocab) pr[i] = v[e] >= qc && v[e] > 0.0f ? (double)v[e] / Skept : 0.0;
+            }
+        }
     }
     return 0;
 }

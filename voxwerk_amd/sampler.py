@@ -307,12 +307,13 @@ class Context:
         self._check(rc)
 
     def sample_stats_device(self, rows: int, vocab: int, logits, ld: int, params, params_stride: int, u, out_ids,
-                            stats, hist_off=None, hist_ids=None, path: str = "auto") -> None:
+                            stats, hist_off=None, hist_ids=None, path: str = "auto", probs=None) -> None:
         """vxs_sample_stats_device: ids plus, for rows of the one-wave nucleus regime, [kept fraction,
-        smallest kept probability, kept count, 0] in stats[r] (NaN for other rows)."""
+        smallest kept probability, kept count, 0] in stats[r] (NaN for other rows), and with probs
+        ([rows][vocab] fp64) every entry's final probability for those rows (NaN for other rows)."""
         rc = self._lib.vxs_sample_stats_device(self._h, rows, vocab, ptr(logits), ld, ptr(hist_off), ptr(hist_ids),
                                                ptr(params), params_stride, ptr(u), ptr(out_ids), ptr(stats),
-                                               PATH_FLAGS[path])
+                                               ptr(probs), PATH_FLAGS[path])
         self._check(rc)
 
     def apply_repetition_penalty(self, logits: np.ndarray, hist_off: np.ndarray, hist_ids: np.ndarray,
