@@ -1,0 +1,136 @@
+"""Randomised parity sweep: random batches over every path of the sampler (one-wave, one-workgroup,
+streaming), each compared with the CPU oracle on the same inputs.
+
+A batch draws its vocabulary (7 to 151,936 entries), its row count, the shape of its logits (normal
+at several scales, Zipf-like, integer ties, sparse spikes, the headline's two-component mixture,
+signed zeros), histories of 0 to 5000 ids and per-row options over everything the reference's
+sampler takes (greedy rows, top-k 1-299, top-p from 1e-6 to 1, temperatures 0.3-2, penalties below
+and above 1, suppression ranges with a kept id, a banned id), a forced or automatic path, and for
+some batches the final probabilities. Bar: ids identical except counted boundary draws and cuts,
+probabilities within 1e-5 relative (the bar of tests/test_gpu_parity.py).
+
+    python tests/sweep.py --seconds 300 --seed 1      # long run on a GPU box, one line per batch
+The GPU suite runs a short seeded sweep (tests/test_gpu_sweep.py).
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.dirname(HERE), HERE):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+from oracle import ref  # noqa: E402
+from parity import PROB_RTOL, comparable_rows, compare_ids, prob_rel_error  # noqa: E402
+from voxwerk_amd._lib import PARAMS_DTYPE  # noqa: E402
+
+VOCABS = [7, 64, 300, 1000, 2048, 2500, 3001, 3072, 3072, 3072, 4096, 8192, 9000, 32000, 151936]
+
+
+def random_batch(rng):
+    """One random batch: (logits, params, u, hist_off, hist_ids, path, want_probs, label)."""
+    V = int(rng.choice(VOCABS))
+    if V <= 3072:
+        rows = int(rng.choice([1, 2, 3, 17, 64, 255, 1024, 2049, 4096]))
+    else:
+        rows = int(rng.integers(1, (512 if V <= 32000 else 48) + 1))
+    kind = int(rng.integers(0, 5))
+    if kind == 0:
+        x = rng.standard_normal((rows, V)) * rng.choice([0.3, 1.0, 3.0, 8.0], size=(rows, 1))
+    elif kind == 1:  # Zipf-like: -log(rank), shuffled per row
+        r = np.log(np.arange(1, V + 1))
+        x = np.stack([-r[rng.permutation(V)] * rng.uniform(0.5, 2.0) for _ in range(rows)])
+        x += rng.standard_normal((rows, V)) * 0.1
+    elif kind == 2:  # integer values: many exact ties
+        x = np.round(rng.standard_normal((rows, V)) * rng.choice([1.0, 2.0, 4.0], size=(rows, 1)))
+    elif kind == 3:  # sparse spikes over a normal background
+        x = rng.standard_normal((rows, V))
+        x[rng.random((rows, V)) < 0.01] += rng.uniform(3, 12)
+    else:  # 0.9 N(0, 1) + 0.1 N(4, 1)
+        x = 0.9 * rng.standard_normal((rows, V)) + (4.0 + rng.standard_normal((rows, V))) * (rng.random((rows, V)) < 0.1)
+    x = x.astype(np.float32)
+    if rng.random() < 0.05:  # zeros of both signs
+        z = rng.random((rows, V)) < 0.2
+        x[z] = np.where(rng.random(int(z.sum())) < 0.5, np.float32(0.0), np.float32(-0.0))
+    hmax = int(rng.choice([0, 16, 256, 512, 2048, 3000, 5000]))
+    hl = rng.integers(0, hmax + 1, size=rows) if hmax else np.zeros(rows, np.int64)
+    off = np.zeros(rows + 1, np.int32)
+    off[1:] = np.cumsum(hl)
+    hist = rng.integers(0, V, size=int(off[-1])).astype(np.int32)
+    p = np.zeros(rows, dtype=PARAMS_DTYPE)
+    p["do_sample"] = (rng.random(rows) > 0.05).astype(np.int32)
+    p["top_k"] = np.where(rng.random(rows) < rng.uniform(0, 1), rng.integers(1, 300, rows), 0)
+    p["top_p"] = rng.choice([1.0, 0.999, 0.99, 0.95, 0.9, 0.8, 0.5, 0.1, 1e-6], size=rows).astype(np.float32)
+    p["temperature"] = rng.choice([0.3, 0.7, 0.9, 1.0, 1.3, 2.0], size=rows).astype(np.float32)
+    p["rep_penalty"] = rng.choice([1.0, 1.05, 1.1, 1.3, 0.9, 2.0], size=rows).astype(np.float32)
+    supp = rng.random(rows) < 0.2
+    sb = rng.integers(0, V, rows)
+    p["supp_begin"] = np.where(supp, sb, 0)
+    p["supp_end"] = np.where(supp, np.minimum(V, sb + rng.integers(1, V + 1, rows)), 0)
+    p["keep_id"] = np.where(supp & (rng.random(rows) < 0.5), rng.integers(0, V, rows), -1)
+    p["ban_id"] = np.where(rng.random(rows) < 0.1, rng.integers(0, V, rows), -1)
+    u = rng.random(rows)
+    path = str(rng.choice(["auto", "auto", "block", "wave"])) if V <= 3072 else "auto"
+    want_probs = bool(rng.random() < 0.15) and rows * V <= 4_000_000
+    label = f"kind {kind} rows {rows} V {V} hmax {hmax} path {path} probs {int(want_probs)}"
+    return x, p, u, off, hist, path, want_probs, label
+
+
+def run_batch(ctx, batch, threads: int = 16):
+    """Sample one batch on the GPU and with the oracle; returns the parity report."""
+    x, p, u, off, hist, path, want_probs, _ = batch
+    out = ctx.sample(x, p, u, off, hist, path=path, raise_on_error=False, want_probs=want_probs)
+    ids = out[0] if isinstance(out, tuple) else out
+    ora = ref.sample(x, p, u, off, hist, threads=threads, want_probs=want_probs)
+    rep = compare_ids(ids, ora)
+    if want_probs:
+        rep.max_prob_rel = prob_rel_error(out[-1], ora["probs"], comparable_rows(ids, ora))
+    return rep
+
+
+def sweep(ctx, seed: int, batches: int = 0, seconds: float = 0.0, threads: int = 16, log=print):
+    """Run `batches` random batches (or as many as fit in `seconds`); stops at the first batch that
+    misses the bar. Returns (totals, failing report or None)."""
+    rng = np.random.default_rng(seed)
+    end = time.time() + seconds
+    tot = {"batches": 0, "rows": 0, "exact": 0, "draw_boundary": 0, "topp_boundary": 0, "max_prob_rel": 0.0}
+    while (batches and tot["batches"] < batches) or (seconds and time.time() < end):
+        batch = random_batch(rng)
+        log(batch[-1])
+        rep = run_batch(ctx, batch, threads)
+        log(f"  {rep}")
+        tot["batches"] += 1
+        tot["rows"] += rep.rows
+        tot["exact"] += rep.exact
+        tot["draw_boundary"] += rep.draw_boundary
+        tot["topp_boundary"] += rep.topp_boundary
+        tot["max_prob_rel"] = max(tot["max_prob_rel"], rep.max_prob_rel)
+        if rep.unexplained or rep.max_prob_rel > PROB_RTOL:
+            return tot, rep
+    return tot, None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--seconds", type=float, default=60.0)
+    ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--threads", type=int, default=16, help="oracle threads (at most one GPU's share of the host)")
+    args = ap.parse_args()
+    from voxwerk_amd.sampler import Context
+
+    ctx = Context(0)
+    tot, bad = sweep(ctx, args.seed, seconds=args.seconds, threads=args.threads, log=lambda s: print(s, flush=True))
+    print("TOTAL", tot, flush=True)
+    if bad is not None:
+        print("FAILED", bad, "rows", bad.unexplained[:20], flush=True)
+        sys.exit(1)
+
+
+if __name__ == "__main__":
+    main()

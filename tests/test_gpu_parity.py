@@ -83,6 +83,25 @@ def test_mixed_options(ctx, vocab):
     check(*both(ctx, logits, p, u, off, hist), label=f"mixed V={vocab}")
 
 
+@pytest.mark.parametrize("vocab", [3072, 5000, 9000])
+def test_tiny_probabilities_keep_their_value(ctx, vocab):
+    """Rows whose logits span more than 87 after temperature, so that exp(x - max) of the smallest
+    kept entries is below fp32's normal range (the reference's fp64 Math.Exp still gives them a
+    positive probability, down to d = -745): every probability the oracle keeps, those included,
+    within 1e-5 relative, on the one-workgroup path (3072, 5000) and the streaming path (9000)."""
+    rng = np.random.default_rng(7000 + vocab)
+    rows = 32
+    logits = np.round(rng.standard_normal((rows, vocab)) * 4.0).astype(np.float32)
+    logits[:, ::97] -= 40.0  # a far tail: d down to about -200 at T = 0.3
+    p = _params(rows, rng, top_k=0, rep_penalty=1.0)
+    p["top_p"] = np.where(np.arange(rows) % 2 == 0, 1.0, rng.choice([0.999999, 0.9999], size=rows)).astype(np.float32)
+    p["temperature"] = rng.choice([0.3, 0.5], size=rows).astype(np.float32)
+    ids, lg, pr, ora = both(ctx, logits, p, rng.random(rows))
+    tiny = (ora["probs"] > 0) & (ora["probs"] < 1e-38)
+    assert tiny.sum() > 0, "the rows must hold kept entries below fp32's normal range"
+    check(ids, lg, pr, ora, label=f"tiny probabilities V={vocab}")
+
+
 def test_greedy_ties_and_signed_zero(ctx):
     x = np.array([[0.0, -0.0, 0.0, -1.0], [-0.0, 0.0, -5.0, -0.0], [1.0, 3.0, 3.0, 2.0]], dtype=np.float32)
     p = make_params(SamplingOptions.Greedy())

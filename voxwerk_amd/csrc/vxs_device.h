@@ -808,5 +808,11 @@ __device__ __forceinline__ float exp_neg_unclamped(float d) {
     return __builtin_fmaf(e, yl * kLn2, e);
 }
 
+// exp(d) for d <= 0 as a probability's numerator in fp64: the fp32 form where its result is a normal
+// number (relative error about 1e-7), the fp64 exponential below that (d < -87, where the fp32 form
+// returns 0 and the reference's fp64 Math.Exp still gives a positive value, down to its own
+// underflow at d = -745.13).
+__device__ __forceinline__ double exp_neg_prob(float d) { return d >= -87.0f ? (double)exp_neg(d) : exp((double)d); }
+
 }  // namespace dev
 }  // namespace vxs

@@ -1366,11 +1366,11 @@ __device__ __forceinline__ void row_block(const SampleArgs& a, int vec, int r, R
         double se = 0.0;
 #pragma unroll
         for (int e = 0; e < NE; e++)
-            if (kept(e)) se += (double)exp_neg(v[e]);
+            if (kept(e)) se += exp_neg_prob(v[e]);
         se = g.dsum(se, kSitePSum);
 #pragma unroll
         for (int e = 0; e < NE; e++)
-            if (eidx(e) < V) prow[eidx(e)] = kept(e) ? (double)exp_neg(v[e]) / se : 0.0;
+            if (eidx(e) < V) prow[eidx(e)] = kept(e) ? exp_neg_prob(v[e]) / se : 0.0;
     }
 }
 

@@ -862,12 +862,12 @@ __device__ __forceinline__ void wide_general_row(const SampleArgs& a, int vec, i
         double se = 0.0;
         for_row(xrow, V, vec, g.t, X, [&](int i, float x) {
             const float v = val(i, x);
-            if (kept(i, v)) se += (double)exp_neg(v - mx);
+            if (kept(i, v)) se += exp_neg_prob(v - mx);
         });
         se = g.dsum(se);
         for_row(xrow, V, vec, g.t, X, [&](int i, float x) {
             const float v = val(i, x);
-            prow[i] = kept(i, v) ? (double)exp_neg(v - mx) / se : 0.0;
+            prow[i] = kept(i, v) ? exp_neg_prob(v - mx) / se : 0.0;
         });
     }
 }
