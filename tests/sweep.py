@@ -5,8 +5,10 @@ A batch draws its vocabulary (7 to 151,936 entries), its row count, the shape of
 at several scales, Zipf-like, integer ties, sparse spikes, the headline's two-component mixture,
 signed zeros), histories of 0 to 5000 ids and per-row options over everything the reference's
 sampler takes (greedy rows, top-k 1-299, top-p from 1e-6 to 1, temperatures 0.3-2, penalties below
-and above 1, suppression ranges with a kept id, a banned id), a forced or automatic path, and for
-some batches the final probabilities. Bar: ids identical except counted boundary draws and cuts,
+and above 1, suppression ranges with a kept id, a banned id), some rows outside the contract (NaN
+or +inf logits, a history id past the vocabulary: their error codes must match), a forced or
+automatic path, and for some batches the final probabilities or the write-back logits. Bar: ids and
+error codes identical except counted boundary draws and cuts, write-back logits bit-identical,
 probabilities within 1e-5 relative (the bar of tests/test_gpu_parity.py).
 
     python tests/sweep.py --seconds 300 --seed 1      # long run on a GPU box, one line per batch
@@ -34,7 +36,7 @@ VOCABS = [7, 64, 300, 1000, 2048, 2500, 3001, 3072, 3072, 3072, 4096, 8192, 9000
 
 
 def random_batch(rng):
-    """One random batch: (logits, params, u, hist_off, hist_ids, path, want_probs, label)."""
+    """One random batch: (logits, params, u, hist_off, hist_ids, path, want_probs, want_logits, label)."""
     V = int(rng.choice(VOCABS))
     if V <= 3072:
         rows = int(rng.choice([1, 2, 3, 17, 64, 255, 1024, 2049, 4096]))
@@ -75,22 +77,36 @@ def random_batch(rng):
     p["supp_end"] = np.where(supp, np.minimum(V, sb + rng.integers(1, V + 1, rows)), 0)
     p["keep_id"] = np.where(supp & (rng.random(rows) < 0.5), rng.integers(0, V, rows), -1)
     p["ban_id"] = np.where(rng.random(rows) < 0.1, rng.integers(0, V, rows), -1)
+    if rng.random() < 0.05:  # rows outside the contract: NaN or +inf logits, a history id past V
+        for r in rng.integers(0, rows, size=int(rng.integers(1, 4))):
+            x[r, rng.integers(0, V)] = rng.choice([np.nan, np.inf])
+        if hist.size:
+            hist[rng.integers(0, hist.size)] = V + int(rng.integers(0, 3))
     u = rng.random(rows)
     path = str(rng.choice(["auto", "auto", "block", "wave"])) if V <= 3072 else "auto"
-    want_probs = bool(rng.random() < 0.15) and rows * V <= 4_000_000
-    label = f"kind {kind} rows {rows} V {V} hmax {hmax} path {path} probs {int(want_probs)}"
-    return x, p, u, off, hist, path, want_probs, label
+    small = rows * V <= 4_000_000
+    want_probs = bool(rng.random() < 0.15) and small
+    want_logits = bool(rng.random() < 0.15) and small
+    label = (f"kind {kind} rows {rows} V {V} hmax {hmax} path {path} probs {int(want_probs)} "
+             f"logits {int(want_logits)}")
+    return x, p, u, off, hist, path, want_probs, want_logits, label
 
 
 def run_batch(ctx, batch, threads: int = 16):
-    """Sample one batch on the GPU and with the oracle; returns the parity report."""
-    x, p, u, off, hist, path, want_probs, _ = batch
-    out = ctx.sample(x, p, u, off, hist, path=path, raise_on_error=False, want_probs=want_probs)
+    """Sample one batch on the GPU and with the oracle; returns the parity report (write-back
+    logits that differ from the oracle's on a row that did not fail count as unexplained)."""
+    x, p, u, off, hist, path, want_probs, want_logits, _ = batch
+    out = ctx.sample(x, p, u, off, hist, path=path, raise_on_error=False, want_probs=want_probs,
+                     want_logits=want_logits)
     ids = out[0] if isinstance(out, tuple) else out
-    ora = ref.sample(x, p, u, off, hist, threads=threads, want_probs=want_probs)
+    ora = ref.sample(x, p, u, off, hist, threads=threads, want_probs=want_probs, want_logits=want_logits)
     rep = compare_ids(ids, ora)
     if want_probs:
-        rep.max_prob_rel = prob_rel_error(out[-1], ora["probs"], comparable_rows(ids, ora))
+        rep.max_prob_rel = prob_rel_error(out[2], ora["probs"], comparable_rows(ids, ora) & (ora["ids"] >= 0))
+    if want_logits:
+        ok = ora["ids"] >= 0
+        same = (out[1].view(np.uint32) == ora["logits"].view(np.uint32)).all(axis=1)
+        rep.unexplained += [int(r) for r in np.nonzero(ok & ~same)[0] if int(r) not in rep.unexplained]
     return rep
 
 
