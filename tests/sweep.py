@@ -7,7 +7,9 @@ signed zeros), histories of 0 to 5000 ids and per-row options over everything th
 sampler takes (greedy rows, top-k 1-299, top-p from 1e-6 to 1, temperatures 0.3-2, penalties below
 and above 1, suppression ranges with a kept id, a banned id), some rows outside the contract (NaN
 or +inf logits, a history id past the vocabulary: their error codes must match), a forced or
-automatic path, and for some batches the final probabilities or the write-back logits. Bar: ids and
+automatic path, one of three entry points (host buffers; device buffers with a padded leading
+dimension and possibly a base one float past 16-byte alignment; the entry point that allocates
+nothing), and for some batches the final probabilities or the write-back logits. Bar: ids and
 error codes identical except counted boundary draws and cuts, write-back logits bit-identical,
 probabilities within 1e-5 relative (the bar of tests/test_gpu_parity.py).
 
@@ -36,7 +38,8 @@ VOCABS = [7, 64, 300, 1000, 2048, 2500, 3001, 3072, 3072, 3072, 4096, 8192, 9000
 
 
 def random_batch(rng):
-    """One random batch: (logits, params, u, hist_off, hist_ids, path, want_probs, want_logits, label)."""
+    """One random batch: (logits, params, u, hist_off, hist_ids, path, want_probs, want_logits,
+    (entry point, leading-dimension pad, base shift), label)."""
     V = int(rng.choice(VOCABS))
     if V <= 3072:
         rows = int(rng.choice([1, 2, 3, 17, 64, 255, 1024, 2049, 4096]))
@@ -87,17 +90,61 @@ def random_batch(rng):
     small = rows * V <= 4_000_000
     want_probs = bool(rng.random() < 0.15) and small
     want_logits = bool(rng.random() < 0.15) and small
+    # the entry point: host buffers (vxs_sample), device buffers with a padded leading dimension and
+    # possibly a base one float past 16-byte alignment (vxs_sample_device), or the entry point that
+    # allocates nothing (vxs_sample_noalloc); the last two return ids only
+    api = "host" if want_probs or want_logits else str(rng.choice(["host", "host", "host", "device", "noalloc"]))
+    pad, shift = int(rng.choice([0, 1, 3, 64])), int(rng.choice([0, 1]))
     label = (f"kind {kind} rows {rows} V {V} hmax {hmax} path {path} probs {int(want_probs)} "
-             f"logits {int(want_logits)}")
-    return x, p, u, off, hist, path, want_probs, want_logits, label
+             f"logits {int(want_logits)} api {api}" + (f" pad {pad} shift {shift}" if api == "device" else ""))
+    return x, p, u, off, hist, path, want_probs, want_logits, (api, pad, shift), label
+
+
+NOALLOC_UNSUPPORTED = -5  # VXS_ERR_UNSUPPORTED: the call does not fit the entry point's scratch
+
+
+def gpu_ids(ctx, batch):
+    """The batch through the chosen entry point; None when vxs_sample_noalloc declines its size."""
+    x, p, u, off, hist, path, want_probs, want_logits, (api, pad, shift), _ = batch
+    rows, V = x.shape
+    if api == "host":
+        return ctx.sample(x, p, u, off, hist, path=path, raise_on_error=False, want_probs=want_probs,
+                          want_logits=want_logits)
+    if api == "noalloc":
+        from voxwerk_amd._lib import ptr
+
+        ids = np.full(rows, -99, np.int32)
+        rc = ctx._lib.vxs_sample_noalloc(ctx.handle, rows, V, ptr(x), V, ptr(off), ptr(hist), ptr(p), 1, ptr(u),
+                                         ptr(ids), 0)
+        if rc == NOALLOC_UNSUPPORTED and (ids == -99).all():
+            return None
+        bad = np.nonzero(ids < 0)[0]
+        assert rc == (int(ids[bad[0]]) if bad.size else 0), (rc, ctx.last_error())  # the lowest failing row's code
+        return ids
+    from voxwerk_amd.hip import DeviceArray
+
+    ld = V + pad
+    buf = np.full(shift + rows * ld, np.nan, np.float32)  # pads hold NaN: never read
+    buf[shift:].reshape(rows, ld)[:, :V] = x
+    arrs = [DeviceArray.from_numpy(a) for a in (buf, p, u, off, hist if hist.size else np.zeros(1, np.int32))]
+    d_ids = DeviceArray((rows,), np.int32)
+    try:
+        ctx.sample_device(rows, V, arrs[0].ptr + 4 * shift, ld, arrs[1], 1, arrs[2], d_ids, arrs[3], arrs[4],
+                          path=path)
+        ctx.synchronize()
+        return d_ids.numpy()
+    finally:
+        for a in arrs + [d_ids]:
+            a.free()
 
 
 def run_batch(ctx, batch, threads: int = 16):
     """Sample one batch on the GPU and with the oracle; returns the parity report (write-back
     logits that differ from the oracle's on a row that did not fail count as unexplained)."""
-    x, p, u, off, hist, path, want_probs, want_logits, _ = batch
-    out = ctx.sample(x, p, u, off, hist, path=path, raise_on_error=False, want_probs=want_probs,
-                     want_logits=want_logits)
+    x, p, u, off, hist, path, want_probs, want_logits = batch[:8]
+    out = gpu_ids(ctx, batch)
+    if out is None:
+        return None
     ids = out[0] if isinstance(out, tuple) else out
     ora = ref.sample(x, p, u, off, hist, threads=threads, want_probs=want_probs, want_logits=want_logits)
     rep = compare_ids(ids, ora)
@@ -120,7 +167,9 @@ def sweep(ctx, seed: int, batches: int = 0, seconds: float = 0.0, threads: int =
         batch = random_batch(rng)
         log(batch[-1])
         rep = run_batch(ctx, batch, threads)
-        log(f"  {rep}")
+        log(f"  {rep}" if rep is not None else "  (larger than the no-alloc scratch: skipped)")
+        if rep is None:
+            continue
         tot["batches"] += 1
         tot["rows"] += rep.rows
         tot["exact"] += rep.exact
