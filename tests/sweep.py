@@ -14,7 +14,12 @@ error codes identical except counted boundary draws and cuts, write-back logits 
 probabilities within 1e-5 relative (the bar of tests/test_gpu_parity.py).
 
     python tests/sweep.py --seconds 300 --seed 1      # long run on a GPU box, one line per batch
-The GPU suite runs a short seeded sweep (tests/test_gpu_sweep.py).
+    python tests/sweep.py --heads 500 --seconds 0     # random logit-head calls (bf16 and int8)
+The GPU suite runs a short seeded sweep of each (tests/test_gpu_sweep.py). Head calls: rows 1-64,
+k a multiple of 8 up to 2048, n up to 5200, padded leading dimensions, bf16 or int8 weights (packed
+on the GPU, bit-identical to the oracle's packing), real, integer-valued or partly non-finite hidden
+values; bar: within the fp32 bound of the exact product (exact on integer data), the IEEE pattern
+of non-finite results, nothing written past n.
 """
 from __future__ import annotations
 
@@ -181,15 +186,110 @@ def sweep(ctx, seed: int, batches: int = 0, seconds: float = 0.0, threads: int =
     return tot, None
 
 
+def random_head_case(rng):
+    """One random logit-head call: rows, k (a multiple of 8 up to 2048), n, leading-dimension pads,
+    bf16 or int8 weights, real, integer-valued or partly non-finite hidden values."""
+    rows = int(rng.choice([1, 2, 3, 5, 8, 9, 16, 24, 31, 32, 33, 48, 64]))
+    k = 8 * int(rng.integers(1, 257))
+    n = int(rng.integers(1, 400)) if rng.random() < 0.4 else int(rng.integers(2000, 5200))
+    data = str(rng.choice(["real", "real", "integer", "nonfinite"]))
+    return dict(rows=rows, k=k, n=n, padx=4 * int(rng.integers(0, 5)), padw=8 * int(rng.integers(0, 3)),
+                pado=int(rng.integers(0, 9)), int8=bool(rng.random() < 0.3), data=data,
+                seed=int(rng.integers(0, 2**31)))
+
+
+def run_head_case(ctx, c) -> str:
+    """Run one head call on the GPU and check it against the oracle; returns '' or what failed."""
+    from oracle.head_np import head_bound, head_exact, head_int8_bound, head_int8_exact, pack_int8
+    from voxwerk_amd.hip import DeviceArray
+
+    rng = np.random.default_rng(c["seed"])
+    rows, k, n = c["rows"], c["k"], c["n"]
+    ldx, ldw, ldo = k + c["padx"], k + c["padw"], n + c["pado"]
+    if c["data"] == "integer":
+        x = rng.integers(-8, 9, (rows, k)).astype(np.float32)
+        wf = rng.integers(-8, 9, (n, k)).astype(np.float32)
+    else:
+        x = rng.standard_normal((rows, k)).astype(np.float32)
+        wf = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    if c["data"] == "nonfinite":
+        for _ in range(int(rng.integers(1, 4))):
+            x[rng.integers(0, rows), rng.integers(0, k)] = rng.choice([np.inf, -np.inf, np.nan])
+    w = (wf.view(np.uint32) >> 16).astype(np.uint16)
+    xp = np.zeros((rows, ldx), np.float32)
+    xp[:, :k] = x
+    wp = np.zeros((n, ldw), np.uint16)
+    wp[:, :k] = w
+    arrs = [DeviceArray.from_numpy(xp), DeviceArray.from_numpy(wp),
+            DeviceArray.from_numpy(np.full((rows, ldo), 7.0, np.float32))]
+    try:
+        if c["int8"]:
+            d_q = DeviceArray.from_numpy(np.full((n, ldw), 99, np.int8))
+            d_s = DeviceArray((n,), np.float32)
+            arrs += [d_q, d_s]
+            ctx.head_pack_int8_device(k, n, arrs[1], ldw, d_q, ldw, d_s)
+            ctx.head_int8_device(rows, k, n, arrs[0], ldx, d_q, ldw, d_s, arrs[2], ldo)
+        else:
+            ctx.head_device(rows, k, n, arrs[0], ldx, arrs[1], ldw, arrs[2], ldo)
+        ctx.synchronize()
+        out = arrs[2].numpy()
+        if c["int8"]:
+            q, scale = d_q.numpy()[:, :k], d_s.numpy()
+    finally:
+        for a in arrs:
+            a.free()
+    if not np.all(out[:, n:] == 7.0):
+        return "wrote past n"
+    got = out[:, :n].astype(np.float64)
+    if c["int8"]:
+        wq, ws = pack_int8(w)
+        if not (np.array_equal(q, wq) and np.array_equal(scale.view(np.uint32), ws.view(np.uint32))):
+            return "int8 packing differs from the oracle's"
+        exact, bound = head_int8_exact(x, q, scale), head_int8_bound(x, q, scale)
+    else:
+        with np.errstate(invalid="ignore", over="ignore"):
+            exact, bound = head_exact(x, w), head_bound(x, w)
+    fin = np.isfinite(exact)
+    for cls in (np.isnan, np.isposinf, np.isneginf):
+        if not np.array_equal(cls(got), cls(exact)):
+            return f"non-finite pattern differs ({cls.__name__})"
+    if c["data"] == "integer" and not c["int8"] and not np.array_equal(got, exact):
+        return "integer data not exact"
+    err = np.abs(got[fin] - exact[fin])
+    if not np.all(err <= bound[fin]):
+        return f"outside the fp32 bound (max err/bound {np.max(err / np.maximum(bound[fin], 1e-300)):.3f})"
+    return ""
+
+
+def head_sweep(ctx, seed: int, cases: int, log=print) -> list:
+    """`cases` random head calls; returns the failing cases with what failed."""
+    rng = np.random.default_rng(seed)
+    bad = []
+    for _ in range(cases):
+        c = random_head_case(rng)
+        log(f"head {c}")
+        why = run_head_case(ctx, c)
+        if why:
+            log(f"  FAILED: {why}")
+            bad.append((c, why))
+    return bad
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--seconds", type=float, default=60.0)
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--threads", type=int, default=16, help="oracle threads (at most one GPU's share of the host)")
+    ap.add_argument("--heads", type=int, default=0, help="random logit-head calls to check first")
     args = ap.parse_args()
     from voxwerk_amd.sampler import Context
 
     ctx = Context(0)
+    if args.heads:
+        bad = head_sweep(ctx, args.seed, args.heads, log=lambda s: print(s, flush=True))
+        print(f"HEADS {args.heads} calls, {len(bad)} failed", flush=True)
+        if bad:
+            sys.exit(1)
     tot, bad = sweep(ctx, args.seed, seconds=args.seconds, threads=args.threads, log=lambda s: print(s, flush=True))
     print("TOTAL", tot, flush=True)
     if bad is not None:

@@ -1,8 +1,9 @@
 """GPU: a seeded randomised parity sweep (tests/sweep.py) over every path of the sampler against the
-oracle: ids identical except counted boundary draws and cuts, probabilities within 1e-5 relative."""
+oracle: ids identical except counted boundary draws and cuts, probabilities within 1e-5 relative;
+and random logit-head calls within the fp32 bound of the exact product."""
 import pytest
 
-from sweep import sweep
+from sweep import head_sweep, sweep
 
 pytestmark = pytest.mark.gpu
 
@@ -12,3 +13,8 @@ def test_random_sweep(ctx, seed):
     tot, bad = sweep(ctx, seed, batches=120, threads=8, log=lambda s: print(s, flush=True))
     print(f"seed {seed}: {tot}", flush=True)
     assert bad is None, f"seed {seed}: {bad} rows {bad.unexplained[:10]}"
+
+
+def test_random_head_sweep(ctx):
+    bad = head_sweep(ctx, 201, 80, log=lambda s: print(s, flush=True))
+    assert not bad, bad[:3]
