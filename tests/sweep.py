@@ -15,6 +15,7 @@ probabilities within 1e-5 relative (the bar of tests/test_gpu_parity.py).
 
     python tests/sweep.py --seconds 300 --seed 1      # long run on a GPU box, one line per batch
     python tests/sweep.py --heads 500 --seconds 0     # random logit-head calls (bf16 and int8)
+    python tests/sweep.py --sequences 50 --seconds 0  # random batched stages over a history store
 The GPU suite runs a short seeded sweep of each (tests/test_gpu_sweep.py). Head calls: rows 1-64,
 k a multiple of 8 up to 2048, n up to 5200, padded leading dimensions, bf16 or int8 weights (packed
 on the GPU, bit-identical to the oracle's packing), real, integer-valued or partly non-finite hidden
@@ -275,12 +276,98 @@ def head_sweep(ctx, seed: int, cases: int, log=print) -> list:
     return bad
 
 
+def _i32(v: int) -> int:
+    return ((v + 0x80000000) & 0xFFFFFFFF) - 0x80000000
+
+
+def batch_sequence(ctx, seed: int, log=print) -> str:
+    """One random sequence of batched stages over a resident history store (vxs_sample_batch): slots
+    with random initial histories and seeds, then 3-12 stages, each over a random subset of the
+    slots in a random order, with random options, append on or off and the uniforms from the host or
+    from the slots' device generators. Each stage's ids must equal the CSR-history call on the
+    host's copy of the histories (same kernels) and the oracle's (counted boundaries aside); after
+    the sequence every slot's history must equal the host copy and every generator must continue as
+    .NET's Random(seed) / Random(seed + 1) does. Returns '' or what failed."""
+    from voxwerk_amd.sampler import DotNetRandom
+
+    rng = np.random.default_rng(seed)
+    nslots = int(rng.integers(1, 65))
+    steps = int(rng.integers(3, 13))
+    cap = int(rng.integers(steps + 1, 3000))
+    V = int(rng.choice([2048, 3072, 3072, 8192, 151936]))
+    maxrows = nslots if V <= 8192 else min(nslots, 8)
+    hist = [list(rng.integers(0, V, size=int(rng.integers(0, cap - steps + 1)))) for _ in range(nslots)]
+    seeds = [int(v) for v in rng.integers(-2**31, 2**31, nslots)]
+    gens = {(s, st): DotNetRandom(sd if st == "talker" else _i32(sd + 1))
+            for s, sd in enumerate(seeds) for st in ("talker", "sub")}
+    log(f"batch sequence: {nslots} slots, cap {cap}, {steps} stages, V {V}")
+    with ctx.history(nslots, cap) as store:
+        for s in range(nslots):
+            store.set(s, hist[s])
+            store.seed(s, seeds[s])
+        for t in range(steps):
+            rows = int(rng.integers(1, maxrows + 1))
+            slots = rng.permutation(nslots)[:rows].astype(np.int32)
+            x = (rng.standard_normal((rows, V)) * rng.choice([1.0, 3.0])).astype(np.float32)
+            x[:, :64] += 3.0  # ids the histories often hold: the penalty decides draws
+            p = np.zeros(rows, dtype=PARAMS_DTYPE)
+            p["do_sample"] = (rng.random(rows) > 0.1).astype(np.int32)
+            p["top_k"] = rng.choice([0, 1, 20, 50, 256, 300], size=rows)
+            p["top_p"] = rng.choice([1.0, 0.95, 0.8, 0.3], size=rows).astype(np.float32)
+            p["temperature"] = rng.choice([0.7, 0.9, 1.0, 1.3], size=rows).astype(np.float32)
+            p["rep_penalty"] = rng.choice([1.05, 1.3, 0.9, 1.0], size=rows).astype(np.float32)
+            p["supp_begin"], p["supp_end"] = max(V - 1024, 0), V
+            p["keep_id"], p["ban_id"] = min(2150, V - 1), -1
+            append = bool(rng.random() < 0.7)
+            mode = str(rng.choice(["host", "talker", "sub"]))
+            path = str(rng.choice(["auto", "block", "wave"])) if V <= 3072 else "auto"
+            if mode == "host":
+                u = rng.random(rows)
+            else:
+                u = np.array([gens[(int(s), mode)].NextDouble() if p["do_sample"][r] else 0.0
+                              for r, s in enumerate(slots)])
+            off = np.zeros(rows + 1, np.int32)
+            off[1:] = np.cumsum([len(hist[s]) for s in slots])
+            ids_csr = np.array([i for s in slots for i in hist[s]], np.int32)
+            want = ctx.sample(x, p, u, off, ids_csr, path=path)
+            got = ctx.sample_batch(store, x, slots, p, None if mode != "host" else u, append=append, path=path,
+                                   rng=None if mode == "host" else mode)
+            if not np.array_equal(got, want):
+                return f"stage {t} ({mode}, append {append}): resident {got[:8]} vs CSR {want[:8]}"
+            c = ref.classify(got, ref.sample(x, p, u, off, ids_csr))
+            if c["unexplained"]:
+                return f"stage {t}: {c}"
+            if append:
+                for r, s in enumerate(slots):
+                    hist[s].append(int(got[r]))
+        for s in range(nslots):
+            if store.get(s).tolist() != [int(i) for i in hist[s]]:
+                return f"slot {s}: history differs from the host copy"
+            for st in ("talker", "sub"):
+                if store.draw(s, st, 2).tolist() != [gens[(s, st)].NextDouble() for _ in range(2)]:
+                    return f"slot {s}: generator {st} out of step"
+    return ""
+
+
+def batch_sweep(ctx, seed: int, sequences: int, log=print) -> list:
+    rng = np.random.default_rng(seed)
+    bad = []
+    for _ in range(sequences):
+        sd = int(rng.integers(0, 2**31))
+        why = batch_sequence(ctx, sd, log)
+        if why:
+            log(f"  FAILED (sequence seed {sd}): {why}")
+            bad.append((sd, why))
+    return bad
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--seconds", type=float, default=60.0)
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--threads", type=int, default=16, help="oracle threads (at most one GPU's share of the host)")
     ap.add_argument("--heads", type=int, default=0, help="random logit-head calls to check first")
+    ap.add_argument("--sequences", type=int, default=0, help="random batched-stage sequences to check first")
     args = ap.parse_args()
     from voxwerk_amd.sampler import Context
 
@@ -288,6 +375,11 @@ def main():
     if args.heads:
         bad = head_sweep(ctx, args.seed, args.heads, log=lambda s: print(s, flush=True))
         print(f"HEADS {args.heads} calls, {len(bad)} failed", flush=True)
+        if bad:
+            sys.exit(1)
+    if args.sequences:
+        bad = batch_sweep(ctx, args.seed, args.sequences, log=lambda s: print(s, flush=True))
+        print(f"SEQUENCES {args.sequences}, {len(bad)} failed", flush=True)
         if bad:
             sys.exit(1)
     tot, bad = sweep(ctx, args.seed, seconds=args.seconds, threads=args.threads, log=lambda s: print(s, flush=True))

@@ -1,9 +1,10 @@
 """GPU: a seeded randomised parity sweep (tests/sweep.py) over every path of the sampler against the
 oracle: ids identical except counted boundary draws and cuts, probabilities within 1e-5 relative;
-and random logit-head calls within the fp32 bound of the exact product."""
+random logit-head calls within the fp32 bound of the exact product; and random sequences of batched
+stages over a resident history store (ids, histories and device generators against the host's copy)."""
 import pytest
 
-from sweep import head_sweep, sweep
+from sweep import batch_sweep, head_sweep, sweep
 
 pytestmark = pytest.mark.gpu
 
@@ -17,4 +18,9 @@ def test_random_sweep(ctx, seed):
 
 def test_random_head_sweep(ctx):
     bad = head_sweep(ctx, 201, 80, log=lambda s: print(s, flush=True))
+    assert not bad, bad[:3]
+
+
+def test_random_batch_sequences(ctx):
+    bad = batch_sweep(ctx, 301, 6, log=lambda s: print(s, flush=True))
     assert not bad, bad[:3]
