@@ -16,6 +16,7 @@ probabilities within 1e-5 relative (the bar of tests/test_gpu_parity.py).
     python tests/sweep.py --seconds 300 --seed 1      # long run on a GPU box, one line per batch
     python tests/sweep.py --heads 500 --seconds 0     # random logit-head calls (bf16 and int8)
     python tests/sweep.py --sequences 50 --seconds 0  # random batched stages over a history store
+    python tests/sweep.py --stats 200 --seconds 0     # the one-wave kernel's per-entry probabilities
 The GPU suite runs a short seeded sweep of each (tests/test_gpu_sweep.py). Head calls: rows 1-64,
 k a multiple of 8 up to 2048, n up to 5200, padded leading dimensions, bf16 or int8 weights (packed
 on the GPU, bit-identical to the oracle's packing), real, integer-valued or partly non-finite hidden
@@ -276,6 +277,74 @@ def head_sweep(ctx, seed: int, cases: int, log=print) -> list:
     return bad
 
 
+def run_stats_batch(ctx, batch, counts=None) -> str:
+    """The batch (vocabulary <= 3072) through the one-wave kernel's statistics build
+    (vxs_sample_stats_device): ids equal to the timed kernel's (vxs_sample_device) and classified
+    against the oracle; for the rows the one-wave nucleus regime samples, every entry's final
+    probability against the oracle's: within 1e-5 relative above 2^-F * 1e5 (masses live on a 2^-F
+    grid of exp(d)), within one grid step absolute everywhere, the kept sets equal except entries
+    below one step; NaN for every other row. Returns '' or what failed."""
+    from voxwerk_amd.hip import DeviceArray
+
+    x, p, u, off, hist = batch[:5]
+    rows, V = x.shape
+    arrs = [DeviceArray.from_numpy(np.ascontiguousarray(a)) for a in (x, p, u, off, hist if hist.size else off)]
+    d_ids, d_ids2 = DeviceArray((rows,), np.int32), DeviceArray((rows,), np.int32)
+    d_st, d_pr = DeviceArray((rows, 4), np.float64), DeviceArray((rows, V), np.float64)
+    try:
+        ctx.sample_stats_device(rows, V, arrs[0], V, arrs[1], 1, arrs[2], d_ids, d_st, arrs[3], arrs[4], path="wave",
+                                probs=d_pr)
+        ctx.sample_device(rows, V, arrs[0], V, arrs[1], 1, arrs[2], d_ids2, arrs[3], arrs[4], path="wave")
+        ctx.synchronize()
+        ids, ids2, st, pr = d_ids.numpy(), d_ids2.numpy(), d_st.numpy(), d_pr.numpy()
+    finally:
+        for a in arrs + [d_ids, d_ids2, d_st, d_pr]:
+            a.free()
+    if not np.array_equal(ids, ids2):
+        return "statistics build drew differently from the timed kernel"
+    ora = ref.sample(x, p, u, off, hist, threads=16, want_probs=True)
+    rep = compare_ids(ids, ora)
+    if rep.unexplained:
+        return f"ids: {rep}"
+    wave = st[:, 3] == 0
+    if not np.isnan(pr[~wave]).all():
+        return "probabilities written for rows outside the one-wave nucleus regime"
+    ok = wave & comparable_rows(ids, ora) & (ora["ids"] >= 0)
+    po, pk = ora["probs"][ok], pr[ok]
+    F = min(51, 53 - int(np.ceil(np.log2(V))))
+    big = po >= 2.0 ** -F * 1e5
+    rel = np.abs(pk[big] - po[big]) / po[big]
+    if rel.max(initial=0.0) > 1e-5:
+        return f"probability rel error {rel.max():.3e}"
+    if not np.all(np.abs(pk - po) <= 2.0 ** -F + 1e-5 * po):
+        return "probability abs error beyond one grid step"
+    if not np.all(((pk > 0) == (po > 0)) | (po < 2.0 ** -F)):
+        return "kept sets differ above the grid"
+    if counts is not None:
+        counts["rows"] += int(ok.sum())
+        counts["probabilities"] += int(big.sum())
+    return ""
+
+
+def stats_sweep(ctx, seed: int, batches: int, log=print) -> list:
+    """`batches` random batches of at most 3072 entries through run_stats_batch."""
+    rng = np.random.default_rng(seed)
+    bad, n = [], 0
+    counts = {"rows": 0, "probabilities": 0}
+    while n < batches:
+        b = random_batch(rng)
+        if b[0].shape[1] > 3072 or b[0].shape[0] > 2049:
+            continue
+        n += 1
+        log("stats " + b[-1])
+        why = run_stats_batch(ctx, b, counts)
+        if why:
+            log(f"  FAILED: {why}")
+            bad.append((b[-1], why))
+    log(f"one-wave nucleus rows compared: {counts['rows']}, probabilities above the grid: {counts['probabilities']}")
+    return bad
+
+
 def _i32(v: int) -> int:
     return ((v + 0x80000000) & 0xFFFFFFFF) - 0x80000000
 
@@ -368,6 +437,8 @@ def main():
     ap.add_argument("--threads", type=int, default=16, help="oracle threads (at most one GPU's share of the host)")
     ap.add_argument("--heads", type=int, default=0, help="random logit-head calls to check first")
     ap.add_argument("--sequences", type=int, default=0, help="random batched-stage sequences to check first")
+    ap.add_argument("--stats", type=int, default=0,
+                    help="random batches through the one-wave kernel's statistics build to check first")
     args = ap.parse_args()
     from voxwerk_amd.sampler import Context
 
@@ -375,6 +446,11 @@ def main():
     if args.heads:
         bad = head_sweep(ctx, args.seed, args.heads, log=lambda s: print(s, flush=True))
         print(f"HEADS {args.heads} calls, {len(bad)} failed", flush=True)
+        if bad:
+            sys.exit(1)
+    if args.stats:
+        bad = stats_sweep(ctx, args.seed, args.stats, log=lambda s: print(s, flush=True))
+        print(f"STATS {args.stats} batches, {len(bad)} failed", flush=True)
         if bad:
             sys.exit(1)
     if args.sequences:

@@ -1,10 +1,11 @@
 """GPU: a seeded randomised parity sweep (tests/sweep.py) over every path of the sampler against the
 oracle: ids identical except counted boundary draws and cuts, probabilities within 1e-5 relative;
 random logit-head calls within the fp32 bound of the exact product; and random sequences of batched
-stages over a resident history store (ids, histories and device generators against the host's copy)."""
+stages over a resident history store (ids, histories and device generators against the host's copy);
+and random batches through the one-wave kernel's statistics build (per-entry probabilities)."""
 import pytest
 
-from sweep import batch_sweep, head_sweep, sweep
+from sweep import batch_sweep, head_sweep, stats_sweep, sweep
 
 pytestmark = pytest.mark.gpu
 
@@ -23,4 +24,9 @@ def test_random_head_sweep(ctx):
 
 def test_random_batch_sequences(ctx):
     bad = batch_sweep(ctx, 301, 6, log=lambda s: print(s, flush=True))
+    assert not bad, bad[:3]
+
+
+def test_random_stats_batches(ctx):
+    bad = stats_sweep(ctx, 401, 30, log=lambda s: print(s, flush=True))
     assert not bad, bad[:3]
