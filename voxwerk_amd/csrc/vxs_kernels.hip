@@ -25,6 +25,7 @@
 //                floor(u * kept mass) only revisits the one sweep that contains it.
 //
 // Per-row errors are reported in out_ids[row] as negative VXS_ERR_* codes.
+#include <atomic>
 #include <math.h>
 #include <stdint.h>
 
@@ -1447,17 +1448,18 @@ hipError_t launch_nc(const SampleArgs& a, int vec, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// Compute units of the current device (cached per device).
+// Compute units of the current device (cached per device; calls from several threads may each
+// query it once, and store the same value).
 int device_cus() {
-    static int cus[64] = {};
+    static std::atomic<int> cus[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
-        int n = 0;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (!n) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cus[dev] = n;
+        cus[dev].store(n, std::memory_order_relaxed);
     }
-    return cus[dev];
+    return n;
 }
 
 template <int NS, int NC>
