@@ -13,7 +13,7 @@ nothing), and for some batches the final probabilities or the write-back logits.
 error codes identical except counted boundary draws and cuts, write-back logits bit-identical,
 probabilities within 1e-5 relative (the bar of tests/test_gpu_parity.py).
 
-    python tests/sweep.py --seconds 300 --seed 1      # long run on a GPU box, one line per batch
+    python tests/sweep.py --seconds 300 --seed 1      # a long run on the GPU, one line per batch
     python tests/sweep.py --heads 500 --seconds 0     # random logit-head calls (bf16 and int8)
     python tests/sweep.py --sequences 50 --seconds 0  # random batched stages over a history store
     python tests/sweep.py --stats 200 --seconds 0     # the one-wave kernel's per-entry probabilities
