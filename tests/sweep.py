@@ -17,6 +17,7 @@ probabilities within 1e-5 relative (the bar of tests/test_gpu_parity.py).
     python tests/sweep.py --heads 500 --seconds 0     # random logit-head calls (bf16 and int8)
     python tests/sweep.py --sequences 50 --seconds 0  # random batched stages over a history store
     python tests/sweep.py --stats 200 --seconds 0     # the one-wave kernel's per-entry probabilities
+    python tests/sweep.py --misc 200 --seconds 0      # penalty and argmax host calls
 The GPU suite runs a short seeded sweep of each (tests/test_gpu_sweep.py). Head calls: rows 1-64,
 k a multiple of 8 up to 2048, n up to 5200, padded leading dimensions, bf16 or int8 weights (packed
 on the GPU, bit-identical to the oracle's packing), real, integer-valued or partly non-finite hidden
@@ -345,6 +346,49 @@ def stats_sweep(ctx, seed: int, batches: int, log=print) -> list:
     return bad
 
 
+def misc_sweep(ctx, seed: int, calls: int, log=print) -> list:
+    """Random calls of the two other host entry points against the oracle: vxs_apply_repetition_penalty
+    (rows 1-64, vocabularies up to 151,936, histories with repeats, penalties below, at and above 1
+    and extreme ones, logits with zeros of both signs and subnormals): the rows bit-identical;
+    vxs_argmax (ties, -inf entries, all -inf rows): the ids identical. Returns the failing calls."""
+    rng = np.random.default_rng(seed)
+    bad = []
+    for _ in range(calls):
+        V = int(rng.choice(VOCABS))
+        rows = int(rng.integers(1, 65 if V <= 32000 else 5))
+        x = (rng.standard_normal((rows, V)) * rng.choice([0.5, 3.0, 30.0])).astype(np.float32)
+        if rng.random() < 0.3:
+            x = np.round(x)
+        special = rng.random((rows, V))
+        x[special < 0.01] = np.float32(0.0)
+        x[(special >= 0.01) & (special < 0.02)] = np.float32(-0.0)
+        x[(special >= 0.02) & (special < 0.025)] = np.float32(1e-40)  # subnormal
+        what = str(rng.choice(["penalty", "argmax"]))
+        log(f"{what} rows {rows} V {V}")
+        if what == "penalty":
+            hl = rng.integers(0, 3000, size=rows)
+            off = np.zeros(rows + 1, np.int32)
+            off[1:] = np.cumsum(hl)
+            hist = rng.integers(0, min(V, int(rng.choice([64, V]))), size=int(off[-1])).astype(np.int32)
+            rho = float(rng.choice([1.0, 1.05, 1.3, 0.9, 2.0, 1e-30, 1e30, -1.5]))
+            got, want = x.copy(), x.copy()
+            ctx.apply_repetition_penalty(got, off, hist, rho)
+            rc = ref.apply_penalty(want, off, hist, rho)
+            if rc != 0 or not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
+                log(f"  FAILED: penalty {rho} (oracle rc {rc})")
+                bad.append(("penalty", rows, V, rho))
+        else:
+            x[rng.random((rows, V)) < 0.05] = -np.inf
+            if rows > 1 and rng.random() < 0.2:
+                x[0] = -np.inf
+            got = ctx.argmax(x)
+            want = np.array([ref.argmax(x[r]) for r in range(rows)], np.int32)
+            if not np.array_equal(got, want):
+                log(f"  FAILED: argmax {got[:8]} vs {want[:8]}")
+                bad.append(("argmax", rows, V))
+    return bad
+
+
 def _i32(v: int) -> int:
     return ((v + 0x80000000) & 0xFFFFFFFF) - 0x80000000
 
@@ -437,6 +481,7 @@ def main():
     ap.add_argument("--threads", type=int, default=16, help="oracle threads (at most one GPU's share of the host)")
     ap.add_argument("--heads", type=int, default=0, help="random logit-head calls to check first")
     ap.add_argument("--sequences", type=int, default=0, help="random batched-stage sequences to check first")
+    ap.add_argument("--misc", type=int, default=0, help="random penalty and argmax host calls to check first")
     ap.add_argument("--stats", type=int, default=0,
                     help="random batches through the one-wave kernel's statistics build to check first")
     args = ap.parse_args()
@@ -451,6 +496,11 @@ def main():
     if args.stats:
         bad = stats_sweep(ctx, args.seed, args.stats, log=lambda s: print(s, flush=True))
         print(f"STATS {args.stats} batches, {len(bad)} failed", flush=True)
+        if bad:
+            sys.exit(1)
+    if args.misc:
+        bad = misc_sweep(ctx, args.seed, args.misc, log=lambda s: print(s, flush=True))
+        print(f"MISC {args.misc} calls, {len(bad)} failed", flush=True)
         if bad:
             sys.exit(1)
     if args.sequences:

@@ -2,10 +2,11 @@
 oracle: ids identical except counted boundary draws and cuts, probabilities within 1e-5 relative;
 random logit-head calls within the fp32 bound of the exact product; and random sequences of batched
 stages over a resident history store (ids, histories and device generators against the host's copy);
-and random batches through the one-wave kernel's statistics build (per-entry probabilities)."""
+random batches through the one-wave kernel's statistics build (per-entry probabilities); and random
+penalty and argmax host calls."""
 import pytest
 
-from sweep import batch_sweep, head_sweep, stats_sweep, sweep
+from sweep import batch_sweep, head_sweep, misc_sweep, stats_sweep, sweep
 
 pytestmark = pytest.mark.gpu
 
@@ -29,4 +30,9 @@ def test_random_batch_sequences(ctx):
 
 def test_random_stats_batches(ctx):
     bad = stats_sweep(ctx, 401, 30, log=lambda s: print(s, flush=True))
+    assert not bad, bad[:3]
+
+
+def test_random_penalty_and_argmax_calls(ctx):
+    bad = misc_sweep(ctx, 501, 40, log=lambda s: print(s, flush=True))
     assert not bad, bad[:3]
