@@ -150,3 +150,14 @@ def test_dotnet_random_next_double_range_and_determinism():
     assert 0.0 <= min(xs) and max(xs) < 1.0
     assert abs(np.mean(xs) - 0.5) < 0.01
     assert DotNetRandom(-5).Next() == DotNetRandom(5).Next()  # abs(seed), as .NET does
+
+
+def test_committed_traffic_profile_feeds_the_roofline():
+    """bench.py's roofline.traffic comes from the committed FETCH_SIZE + WRITE_SIZE summary of the
+    headline kernel: it must parse, and lie within a few percent above the algorithmic bytes."""
+    import bench
+
+    traffic = bench.read_traffic()
+    algorithmic = 4096 * (4 * 3072 + 4 * 512 + 4 + 8 + 4)
+    assert traffic is not None, "profiles/traffic_full_vocab_nucleus_4096x3072.txt has no traffic_bytes_per_launch"
+    assert algorithmic <= traffic <= 1.05 * algorithmic, (traffic, algorithmic)
