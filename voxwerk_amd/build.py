@@ -33,14 +33,16 @@ HIP_FLAGS = [
 ]
 HIP_SOURCES = ["vxs_kernels.hip", "vxs_wide.hip", "vxs_history.hip", "vxs_embed.hip", "vxs_head.hip", "vxs_noalloc.hip",
                "vxs_api.cpp"]
-# Per-source flags. The sampling kernels are scheduled by LLVM's max-ILP strategy (same registers, no
-# spills; measured on the same GPU against the default scheduler: headline 4096 x 3072 21.10 ->
-# 20.73 us, batched talker 256 x 3072 12.0-12.3 -> 11.85 us, wide vocabulary 129.3 -> 128.7 us,
-# 24-sequence device step 241.6 -> 239.3 us). The heads keep the default (24 x 1024 -> 2048 measured
-# 6.45 -> 6.6 us with it).
+# Per-source flags. The sampling kernels are scheduled by LLVM's max-ILP strategy with relaxed
+# occupancy targets (same registers, no spills; measured on the same GPU against the default
+# scheduler: headline 4096 x 3072 21.10 -> 20.75 us, batched talker 256 x 3072 12.0-12.3 -> 11.54 us
+# (11.85 with max-ILP alone), wide vocabulary 129.3 -> 128.3 us, 24-sequence device step 241.6 ->
+# 238-239 us). The heads keep the default (24 x 1024 -> 2048 measured 6.45 -> 6.6 us with max-ILP,
+# 7.0 us with max-memory-clause).
+_SAMPLER_SCHED = ["-mllvm", "-amdgpu-sched-strategy=max-ilp", "-mllvm", "-amdgpu-schedule-relaxed-occupancy"]
 SOURCE_FLAGS = {
-    "vxs_kernels.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
-    "vxs_wide.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+    "vxs_kernels.hip": _SAMPLER_SCHED,
+    "vxs_wide.hip": _SAMPLER_SCHED,
 }
 
 
