@@ -1408,7 +1408,7 @@ union QuadSmem {
     RowSmem<NC> row;
 };
 
-template <int NS, int NC, bool kStats>
+template <int NS, int NC, bool kStats, bool kPrio>
 __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void sample_quad_kernel(SampleArgs a,
                                                                                                 int vec) {
     __shared__ QuadSmem<NS, NC> sm;
@@ -1419,8 +1419,9 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void sa
     const int r = r0 + wv;
     // Staggered halves (launch_quad sets the split): when the whole grid is resident at once (at
     // most four workgroups per CU, one wave of each per SIMD), the second half of the workgroups
-    // starts its loads after a delay proportional to the first half's bytes and runs at a lower
-    // wave priority, so the first half's rows arrive first and compute while the second half loads.
+    // starts its loads after a delay proportional to the first half's bytes and issues them at a
+    // lower wave priority, so the first half's rows arrive first and compute while the second half
+    // loads; from then on every wave's priority follows its row's remaining work (kPrio).
     // Larger grids run in several rounds, which stagger by themselves, and take no delay.
     if (a.stagger_sleeps) {
         const bool late = (int)blockIdx.x >= a.stagger_from;
@@ -1428,11 +1429,13 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void sa
         for (int i = 0; late && i < a.stagger_sleeps; i++) __builtin_amdgcn_s_sleep(32);
     }
     int b = 0;
-    if (r < a.rows) b = wave_fast_row<NS, kStats>(a, vec, r, lane, sm.wave[wv]);
+    if (r < a.rows) b = wave_fast_row<NS, kStats, kPrio>(a, vec, r, lane, sm.wave[wv]);
     if (lane == 0) back[wv] = b;
     __syncthreads();  // every wave is done with its LDS, and the flags are visible
     const int b0 = back[0], b1 = back[1], b2 = back[2], b3 = back[3];  // workgroup-uniform
     static_assert(kWaves == 4, "four rows per workgroup");
+    if constexpr (kPrio)
+        if (b0 | b1 | b2 | b3) __builtin_amdgcn_s_setprio(3);  // the slowest rows: all four waves alike
     if (b0) row_block<NC>(a, vec, r0, sm.row);
     if (b0 && (b1 | b2 | b3)) __syncthreads();  // LDS is reused by the next row
     if (b1) row_block<NC>(a, vec, r0 + 1, sm.row);
@@ -1474,14 +1477,22 @@ hipError_t launch_quad(const SampleArgs& a_in, int vec, hipStream_t stream) {
     const int g = (int)grid.x, cus = device_cus();
     a.stagger_from = g;
     a.stagger_sleeps = 0;
+    // Priority by remaining work (the kPrio instance) for a grid resident in one round with more
+    // than one workgroup per CU (measured, 3072-entry rows, with / without: 2048 rows 14.8 / 15.2
+    // us, 3072 rows 17.3 / 18.0, 4096 rows 19.7 / 20.7); a grid of several rounds is faster with
+    // the oldest waves first (6144 rows 31.8 / 28.6 us), as they free the slots the next
+    // workgroups wait for.
+    const bool prio = g > cus && g <= 4 * cus;
     if (g <= 4 * cus && g >= 3 * cus) {
         a.stagger_from = g / 2;
         a.stagger_sleeps = (3 * g + 2 * cus) / (4 * cus);
     }
     if (a.out_stats)  // a separate instance, so the statistics cost the sampling kernel nothing
-        hipLaunchKernelGGL((sample_quad_kernel<NS, NC, true>), grid, dim3(kT), 0, stream, a, vec);
+        hipLaunchKernelGGL((sample_quad_kernel<NS, NC, true, false>), grid, dim3(kT), 0, stream, a, vec);
+    else if (prio)
+        hipLaunchKernelGGL((sample_quad_kernel<NS, NC, false, true>), grid, dim3(kT), 0, stream, a, vec);
     else
-        hipLaunchKernelGGL((sample_quad_kernel<NS, NC, false>), grid, dim3(kT), 0, stream, a, vec);
+        hipLaunchKernelGGL((sample_quad_kernel<NS, NC, false, false>), grid, dim3(kT), 0, stream, a, vec);
     return hipGetLastError();
 }
 

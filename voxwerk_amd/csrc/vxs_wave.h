@@ -83,6 +83,15 @@ __device__ __forceinline__ uint32_t mbcnt(uint64_t bal) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
 }
 
+// The wave's issue priority at a step of its row, in the instance that steps it (kPrio): 3 once
+// the row's loads are issued, 2 after the masses, 1 at the crossing bucket, 0 at the draw, so a
+// SIMD issues first for the rows with the most work left instead of for its oldest waves. A
+// compile-time switch: a run-time test would split the code into more scheduling regions.
+template <bool kPrio, int L>
+__device__ __forceinline__ void row_prio() {
+    if constexpr (kPrio) __builtin_amdgcn_s_setprio(L);
+}
+
 }  // namespace wave
 
 template <int NS>
@@ -155,7 +164,7 @@ __device__ __forceinline__ int wave_prepare(const SampleArgs& a, int r, int lane
 
 // Second half: samples row r from its loaded logits. Returns 0 when the row is done (its id
 // written) and 1, having written nothing, when it must go to the general algorithm.
-template <int NS, bool kStats>
+template <int NS, bool kStats, bool kPrio>
 __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane, const vxs_params& P, WaveRow<NS>& w,
                                            WaveSmem<NS>& sm) {
     using namespace wave;
@@ -171,6 +180,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
     const bool pen_on = w.pen_on;
     // entries past the vocabulary (pads) hold -inf: they never win, carry no mass, are never written
 
+    row_prio<kPrio, 3>();  // the row's loads are issued: all of its work is ahead
     // ---- S1: repetition penalty over the distinct history ids
     // Per staged part, every lane first reads the original logit of each of its ids, then writes
     // the penalised value back: a wave's LDS operations execute in order, so all reads precede all
@@ -605,6 +615,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
             }
         }
         wsync();
+        row_prio<kPrio, 2>();
         // mass in units of 2^-F of packed entries (one bucket's, or a sum over buckets) of lane bl,
         // whose values are (2^23 + mantissa of the lane's smallest) + offset, times 2^(exponent - 150)
         auto packed_units = [&](uint32_t bl, uint64_t ent) -> uint64_t {
@@ -654,6 +665,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         // are issued before their ballots are consumed. An entry's 32-bit key is its mass bits
         // above the bucket's smallest (below 2^sh <= 2^19) shifted over its index (12 bits): key
         // order is (mass, index) order inside the bucket.
+        row_prio<kPrio, 1>();
         if (sh > 19) return 1;
         uint32_t n = 0;
         uint32_t gwo = gw;
@@ -774,6 +786,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         Skept = wave_sum(ls);
     }
 
+    row_prio<kPrio, 0>();
     // ---- draw: first index (index order) whose inclusive kept-mass prefix exceeds floor(u * Skept).
     // Per lane and sweep, the kept masses are summed left to right in fp32 (relative error below
     // 2e-7, inside the 1e-6 band where a draw may differ from the reference's); sweep totals and
@@ -886,13 +899,13 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
 }
 
 // Samples row r (r < a.rows) with one wave: 0 when done, 1 when handed back.
-template <int NS, bool kStats>
+template <int NS, bool kStats, bool kPrio>
 __device__ __forceinline__ int wave_fast_row(const SampleArgs& a, int vec, int r, int lane, WaveSmem<NS>& sm) {
     WaveRow<NS> w;
     const vxs_params P = a.params[(int64_t)r * a.params_stride];
     if (wave_prepare<NS>(a, r, lane, P, w)) return 1;
     wave_load_row<NS>(a, vec, r, lane, w);  // after the history loads: measured faster than before them
-    return wave_finish<NS, kStats>(a, r, lane, P, w, sm);
+    return wave_finish<NS, kStats, kPrio>(a, r, lane, P, w, sm);
 }
 
 }  // namespace vxs
