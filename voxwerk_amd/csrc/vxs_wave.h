@@ -84,8 +84,9 @@ __device__ __forceinline__ uint32_t mbcnt(uint64_t bal) {
 }
 
 // The wave's issue priority at a step of its row, in the instance that steps it (kPrio): 3 once
-// the row's loads are issued, 2 after the masses, 1 at the crossing bucket, 0 at the draw, so a
-// SIMD issues first for the rows with the most work left instead of for its oldest waves. A
+// the row's loads are issued; in the nucleus regime 2 after the masses, 1 at the crossing bucket,
+// 0 at the draw; with top-k 2 once the candidates are gathered, 1 at the exact regime. A SIMD
+// then issues first for the rows with the most work left instead of for its oldest waves. A
 // compile-time switch: a run-time test would split the code into more scheduling regions.
 template <bool kPrio, int L>
 __device__ __forceinline__ void row_prio() {
@@ -493,6 +494,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         wsync();
         uint32_t nf = n;
         if (topk_on) {
+            row_prio<kPrio, 2>();  // candidates gathered
             // the exact k-th largest key among the gathered entries (all entries >= it are here)
             uint32_t kq[4];
             float cv[4];
@@ -538,6 +540,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
             fx = cval;  // at most 64 finite entries: every one is a candidate
             fid = cidx;
         }
+        row_prio<kPrio, 1>();  // the exact regime's fp64 chain is what remains
         const double uu = a.u ? a.u[r] : 0.0;
         const float xl = lane < (int)nf ? fx[lane] : 0.0f;
         const int pick = wave_exact(xl, fid, (int)nf, mx, P.top_p < 1.0f, P.top_p, uu, scr, nullptr, lane);
