@@ -1185,6 +1185,11 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
         klo = wave_umin(klo);
         khi = wave_umax(khi);
     }
+    // The row's tail after its pass runs at wave priority 1, and from the rank on at 0: the rows of
+    // the CU still streaming their pass (at turns 2 and 3) keep the issue slots, and the tail fills
+    // the ones they leave (wide workload 128.4 -> 127.0 us; the tail at priorities 3, 2, 1, 0 by
+    // phase measured 128.1, at 0 throughout 127.8).
+    __builtin_amdgcn_s_setprio(1);
     // NaN or fl(M * 1/T) = +inf in a wave's range: the row is checked exactly below
     const bool wbad = wave_any(M != M || M * invT == kPosInf);
     if (g.lane == 0) {
@@ -1287,6 +1292,7 @@ __device__ __forceinline__ bool wide_ordered_row(const SampleArgs& a, int vec, i
         for (int i = g.t; i < V; i += kTW) prow[i] = 0.0;
     __syncthreads();
 
+    __builtin_amdgcn_s_setprio(0);
     // ---- all waves: thread t holds candidate t (index order); its position in (d, index) order,
     // counted over the keys eight at a time, and its exp(d)                        Sampler.cs:57
     if (g.t < n) {
