@@ -85,9 +85,9 @@ __device__ __forceinline__ uint32_t mbcnt(uint64_t bal) {
 
 // The wave's issue priority at a step of its row, in the instance that steps it (kPrio): 3 once
 // the row's loads are issued; in the nucleus regime 2 after the masses, 1 at the crossing bucket,
-// 0 at the draw; with top-k 2 once the candidates are gathered, 1 at the exact regime. A SIMD
-// then issues first for the rows with the most work left instead of for its oldest waves. A
-// compile-time switch: a run-time test would split the code into more scheduling regions.
+// 0 at the draw; with top-k 2 at the gather above the bound, 1 at the k-th value, 0 at the exact
+// regime. A SIMD then issues first for the rows with the most work left instead of for its oldest
+// waves. A compile-time switch: a run-time test would split the code into more scheduling regions.
 template <bool kPrio, int L>
 __device__ __forceinline__ void row_prio() {
     if constexpr (kPrio) __builtin_amdgcn_s_setprio(L);
@@ -454,6 +454,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
             const int slack = min(8, (kL - K) >> 1);
             tf = key2f(wave_bound_regs<1>(lk, wave_umin(lk[0]), wave_umax(lk[0]), K, slack));
         }
+        row_prio<kPrio, 2>();
         // gather the entries >= tf in index order: per sweep, each lane's count (0..4) in a 16-bit
         // field, four sweeps per 64-bit scan
         constexpr int NH = (NS + 3) / 4;
@@ -494,7 +495,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
         wsync();
         uint32_t nf = n;
         if (topk_on) {
-            row_prio<kPrio, 2>();  // candidates gathered
+            row_prio<kPrio, 1>();
             // the exact k-th largest key among the gathered entries (all entries >= it are here)
             uint32_t kq[4];
             float cv[4];
@@ -540,7 +541,7 @@ __device__ __forceinline__ int wave_finish(const SampleArgs& a, int r, int lane,
             fx = cval;  // at most 64 finite entries: every one is a candidate
             fid = cidx;
         }
-        row_prio<kPrio, 1>();  // the exact regime's fp64 chain is what remains
+        row_prio<kPrio, 0>();  // the exact regime's fp64 chain
         const double uu = a.u ? a.u[r] : 0.0;
         const float xl = lane < (int)nf ? fx[lane] : 0.0f;
         const int pick = wave_exact(xl, fid, (int)nf, mx, P.top_p < 1.0f, P.top_p, uu, scr, nullptr, lane);
