@@ -316,14 +316,16 @@ def test_wave_top_k_at_tiny_penalised_logits(ctx):
     run_both_paths(ctx, x, p, u, off, np.concatenate(hist), label="tiny penalised logits at the k-th value")
 
 
-def test_wave_handback_rows_take_one_wave_exact_in_turn(ctx):
+@pytest.mark.parametrize("rows", [1024, 2048])
+def test_wave_handback_rows_take_one_wave_exact_in_turn(ctx, rows):
     """Every row of the batch handed back by the one-wave kernel (more than 256 entries at or above
     the K-th largest lane maximum: five lanes hold only large values), yet with 50 candidates after
     top-k, so each of a workgroup's four rows in turn reaches the one-wave exact regime of the
     one-workgroup algorithm (one wave samples while the others wait for the next row): ids against
-    the oracle and the block path."""
-    rng = np.random.default_rng(5050)
-    rows, vocab = 1024, 3072
+    the oracle and the block path. 1024 rows (one workgroup per CU) run the kernel instance with
+    oldest-first issue, 2048 rows the one whose waves step their priority."""
+    rng = np.random.default_rng(5050 + rows)
+    vocab = 3072
     lane_of = (np.arange(vocab) % 256) // 4  # lane l holds entries c * 256 + 4 l + j
     x = rng.uniform(-3.0, 0.0, (rows, vocab)).astype(np.float32)
     hist = []
